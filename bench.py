@@ -1,0 +1,219 @@
+"""Benchmark of the hip device's hot path on one MI355X; prints ONE JSON line.
+
+Default workload (the north star's headline target): causal flash
+attention, bf16, B=8 H=16 S=4096 D=128, scale 1/sqrt(128), inputs N(0,1) from
+np.random.default_rng(4) drawn in the order q, k, v, dO. One step is one forward and one
+backward over the batch: the three CUSTOM kernels sdpa, sdpa_bwd_q and sdpa_bwd_kv, launched
+back to back on the null stream through the device's runners (the same callables its plans
+call). delta = rowsum(dO * O) is an ordinary reduce in limn's graph; it is computed once before
+timing and reported apart, as the north star's target is for the three CUSTOM kernels.
+
+Work is counted the FlashAttention way (causal = half the square): one causal matmul is
+U = 2*B*H*S*S*D/2; the forward is 2U (QK^T, PV), the backward 5U (S, dP, dV, dK, dQ), so a step
+is 7U = 1.924e12 flop. Per kernel (for the roofline line): sdpa 2U, sdpa_bwd_kv 4U (S, dP, dV,
+dK), sdpa_bwd_q 1U (dQ; its recomputed S and dP are executed, not algorithmic).
+
+Timing: W untimed warmup steps, then K steps between two hipEvents on the null stream with a
+device synchronize on both sides; per-kernel averages come from events recorded between the
+launches of every timed step. The CPU baseline is the oracle's numpy flash attention (a port of
+limn/sdpa.py) on one (b, h) pair of the same inputs, scaled to all B*H pairs.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+MFMA_BF16_PEAK = 2.5e15  # dense bf16 MFMA flop/s, MI355X published
+HBM_PEAK = 8.0e12  # bytes/s
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    return p.parse_args()
+
+
+class Events:
+    """hipEvents on the null stream."""
+
+    def __init__(self, api, n: int):
+        from limn_amd.hip.runtime import check
+
+        self.api, self.check = api, check
+        self.ev = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            check(api.hipEventCreate(ctypes.byref(e)), "creating an event")
+            self.ev.append(e)
+
+    def record(self, i: int) -> None:
+        self.check(self.api.hipEventRecord(self.ev[i], None), "recording an event")
+
+    def ms(self, a: int, b: int) -> float:
+        out = ctypes.c_float()
+        self.check(self.api.hipEventSynchronize(self.ev[b]), "waiting for an event")
+        self.check(self.api.hipEventElapsedTime(ctypes.byref(out), self.ev[a], self.ev[b]), "reading an event")
+        return float(out.value)
+
+
+def cpu_baseline(q, k, v, do, scale: float, B: int, H: int, units: float) -> dict:
+    """The oracle's numpy flash attention (port of limn/sdpa.py) on one (b, h) pair, f32 work,
+    the reference's default block size 16, scaled by B*H."""
+    from oracle import sdpa as ref
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:  # noqa: BLE001
+        cores = 1
+    args = [x[0, 0] for x in (q, k, v)]
+    t0 = time.perf_counter()
+    out, lse = ref.sdpa(*args, causal=True, scale=scale, dtype="bfloat16")
+    delta = (do[0, 0] * out).sum(axis=-1, keepdims=True)
+    ref.sdpa_backward_q(*args, do[0, 0], lse, delta, causal=True, scale=scale, dtype="bfloat16")
+    ref.sdpa_backward_kv(*args, do[0, 0], lse, delta, causal=True, scale=scale, dtype="bfloat16")
+    one = time.perf_counter() - t0
+    seconds = one * B * H
+    return {
+        "value": round(units / seconds / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": int(cores),
+        "kind": "port",
+        "sample": f"numpy oracle (limn/sdpa.py port, block 16) fwd+bwd on 1 of {B * H} (b,h) pairs, {one:.2f} s, scaled x{B * H}",
+    }
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (every box has one MI355X)", file=sys.stderr)
+        return 2
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from limn_amd.dtypes import bf16_bits, bf16_values
+    from limn_amd.hip.device import HipDevice
+    from limn_amd.hip.runtime import hip_unavailable
+    from limn_amd.ops import Node, Op, bfloat16, custom, float32
+
+    reason = hip_unavailable()
+    if reason is not None:
+        raise RuntimeError(f"the hip device is unavailable: {reason}")
+    dev = HipDevice()
+    B, H, S, D = 8, 16, 4096, 128
+    scale = D**-0.5
+    rng = np.random.default_rng(4)
+    host = [bf16_bits(rng.standard_normal((B, H, S, D), dtype=np.float32)) for _ in range(4)]
+
+    def buffer(arr, dtype, shape):
+        buf = dev.alloc(arr.nbytes)
+        dev.copyin(buf, arr)
+        return Node(Op.BUFFER, (), dtype, shape, buf)
+
+    q, k, v, do = (buffer(a, bfloat16, (B, H, S, D)) for a in host)
+    o_node, l_node = custom("sdpa", (q, k, v), (True, scale), ((bfloat16, (B, H, S, D)), (float32, (B, H, S, 1))))
+    fwd = dev.custom_runner(o_node)
+    out, lse = dev.out_alloc(B * H * S * D * 2, False), dev.out_alloc(B * H * S * 4, False)
+    fwd([q.arg, k.arg, v.arg], [out, lse])
+    dev.finish()
+    o_host = bf16_values(dev.copyout(out).view(np.uint16).reshape(B, H, S, D))
+    delta_host = (bf16_values(host[3].reshape(B, H, S, D)) * o_host).sum(axis=-1, keepdims=True).astype(np.float32)
+    delta = buffer(delta_host, float32, (B, H, S, 1))
+    lse_node = Node(Op.BUFFER, (), float32, (B, H, S, 1), lse)
+    srcs = (q, k, v, do, lse_node, delta)
+    (dq_node,) = custom("sdpa_bwd_q", srcs, (True, scale), ((bfloat16, (B, H, S, D)),))
+    dk_node, _ = custom("sdpa_bwd_kv", srcs, (True, scale), ((bfloat16, (B, H, S, D)), (bfloat16, (B, H, S, D))))
+    bwd_q, bwd_kv = dev.custom_runner(dq_node), dev.custom_runner(dk_node)
+    dq, dk, dv = (dev.out_alloc(B * H * S * D * 2, False) for _ in range(3))
+    ins_fwd = [q.arg, k.arg, v.arg]
+    ins_bwd = [q.arg, k.arg, v.arg, do.arg, lse, delta.arg]
+
+    def step():
+        fwd(ins_fwd, [out, lse])
+        bwd_q(ins_bwd, [dq])
+        bwd_kv(ins_bwd, [dk, dv])
+
+    for _ in range(args.warmup):
+        step()
+    dev.finish()
+    ev = Events(dev.api, 2 + 4 * args.steps)
+    per = np.zeros(3)
+    ev.record(0)
+    for s in range(args.steps):
+        base = 2 + 4 * s
+        ev.record(base)
+        fwd(ins_fwd, [out, lse])
+        ev.record(base + 1)
+        bwd_q(ins_bwd, [dq])
+        ev.record(base + 2)
+        bwd_kv(ins_bwd, [dk, dv])
+        ev.record(base + 3)
+    ev.record(1)
+    dev.finish()
+    total_ms = ev.ms(0, 1)
+    for s in range(args.steps):
+        base = 2 + 4 * s
+        per += [ev.ms(base, base + 1), ev.ms(base + 1, base + 2), ev.ms(base + 2, base + 3)]
+    per /= args.steps
+    ms = total_ms / args.steps
+
+    U = 2.0 * B * H * S * S * D / 2
+    step_flops = 7 * U
+    kernel_flops = {"sdpa": 2 * U, "sdpa_bwd_q": 1 * U, "sdpa_bwd_kv": 4 * U}
+    names = ["sdpa", "sdpa_bwd_q", "sdpa_bwd_kv"]
+    dom = int(np.argmax(per))
+    achieved = kernel_flops[names[dom]] / (per[dom] * 1e-3)
+    value = step_flops / (ms * 1e-3)
+    line = {
+        "metric": "sdpa fwd+bwd TFLOP/s & % MFMA peak; fused-kernel HBM GB/s; GPT step tok/s",
+        "value": round(value / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "C4 causal flash attention fwd+bwd (sdpa, sdpa_bwd_q, sdpa_bwd_kv)",
+            "batch": B,
+            "heads": H,
+            "seq_len": S,
+            "head_dim": D,
+            "causal": True,
+            "flop_per_step": step_flops,
+        },
+        "mfma_peak_frac": round(value / MFMA_BF16_PEAK, 4),
+        "kernels_ms": {n: round(float(t), 4) for n, t in zip(names, per)},
+        "roofline": {
+            "kernel": names[dom],
+            "bound": "mfma",
+            "achieved": round(achieved / 1e12, 3),
+            "peak": MFMA_BF16_PEAK / 1e12,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / MFMA_BF16_PEAK, 4),
+            "traffic": None,
+        },
+        "device": {"arch": dev.arch, "compute_units": dev.compute_units},
+    }
+    if not args.no_cpu:
+        inputs = [bf16_values(h.reshape(B, H, S, D)[:1, :1]) for h in host]
+        line["cpu_baseline"] = cpu_baseline(*inputs, scale, B, H, step_flops)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,96 @@
+/*
+ * limn_hip.h - the C ABI of limn's MI355X (gfx950) `hip` device: hand-written CDNA4 kernels
+ * behind plain pointers and sizes.
+ *
+ * limn reaches its GPU kernels through ctypes (reference limn/backend_cuda.py:54-151 binds the
+ * CUDA driver and NVRTC the same way). The generated loop-nest kernels go through hipRTC and
+ * hipModuleLaunchKernel directly; the three fused-attention CUSTOM kernels and the dense
+ * contraction are hand-written and exported here.
+ *
+ * Conventions for every entry point:
+ *  - pointers are device pointers (hipMalloc'd), row-major and contiguous;
+ *  - `dtype` is one of LIMN_HIP_FLOAT64/FLOAT32/FLOAT16/BFLOAT16 and names the storage type of
+ *    q, k, v, dout, key_mask and the outputs; the per-row statistics (lse, delta) are float32
+ *    when dtype is a half width and dtype itself otherwise (limn's accumulate_in);
+ *  - `key_mask` may be NULL; else it is (batch, t_k) of `dtype`, and a zero hides that key;
+ *  - launches are asynchronous on `stream` (NULL = the null stream); return 0 on success, else
+ *    a LIMN_HIP_E* code, with a message from limn_hip_last_error() (thread-local).
+ */
+#ifndef LIMN_HIP_H
+#define LIMN_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LIMN_HIP_ABI_VERSION 1
+
+enum {
+  LIMN_HIP_FLOAT64 = 0,
+  LIMN_HIP_FLOAT32 = 1,
+  LIMN_HIP_FLOAT16 = 2,
+  LIMN_HIP_BFLOAT16 = 3,
+};
+
+enum {
+  LIMN_HIP_OK = 0,
+  LIMN_HIP_EINVAL = 1,       /* arguments that describe no valid call (limn raises ValueError) */
+  LIMN_HIP_EUNSUPPORTED = 2, /* a valid call this library has no kernel for (NotImplementedError) */
+  LIMN_HIP_ERUNTIME = 3,     /* the HIP runtime refused (RuntimeError) */
+};
+
+/* Which ABI this library speaks: LIMN_HIP_ABI_VERSION at build time. */
+int limn_hip_abi_version(void);
+
+/* The message of the last failed call on this thread ("" if none). */
+const char* limn_hip_last_error(void);
+
+/* Properties of HIP device `device` that the limn device checks and reports: its gcn arch
+ * name (e.g. "gfx950:sramecc+:xnack-") into arch[arch_len], compute-unit count, peak clock in
+ * kHz and global memory in bytes. Replaces the capability queries of reference
+ * limn/backend_cuda.py:253-293 (pick_arch, cuDeviceGetAttribute). */
+int limn_hip_device_info(int device, char* arch, int arch_len, int* compute_units, int* clock_khz,
+                         int64_t* global_mem);
+
+/* Which kernel family serves an sdpa call of this shape: 1 = MFMA flash kernels, 0 = the
+ * general-width kernels (any float dtype, any head dims up to 256), -1 = none. */
+int limn_hip_sdpa_path(int dtype, int64_t hd, int64_t hd_v);
+
+/*
+ * Fused attention forward: out = softmax(q k^T * scale [causal: key j <= query i] [key_mask]) v
+ * and lse = the per-row logsumexp of the masked scaled scores.
+ *   q (batch, t_q, hd), k (batch, t_k, hd), v (batch, t_k, hd_v) -> out (batch, t_q, hd_v),
+ *   lse (batch, t_q). A row with every key hidden gives NaN and lse = -inf.
+ * Replaces the CUSTOM "sdpa" kernel of reference limn/cuda_emit.py:921-965, launched by
+ * limn/backend_cuda.py:352-361 (_sdpa_runner); numpy reference limn/sdpa.py:91-137.
+ */
+int limn_hip_sdpa_fwd(const void* q, const void* k, const void* v, const void* key_mask, void* out, void* lse, int dtype,
+                      int64_t batch, int64_t t_q, int64_t t_k, int64_t hd, int64_t hd_v, int causal, double scale,
+                      void* stream);
+
+/*
+ * dQ of fused attention, from p = exp(s*scale - lse) and ds = p (dout v^T - delta) scale:
+ *   dq (batch, t_q, hd) = sum over keys of ds k. delta (batch, t_q) is rowsum(dout * out).
+ * Replaces CUSTOM "sdpa_bwd_q", reference limn/cuda_emit.py:968-1005; numpy reference
+ * limn/sdpa.py:140-170.
+ */
+int limn_hip_sdpa_bwd_q(const void* q, const void* k, const void* v, const void* dout, const void* lse, const void* delta,
+                        const void* key_mask, void* dq, int dtype, int64_t batch, int64_t t_q, int64_t t_k, int64_t hd,
+                        int64_t hd_v, int causal, double scale, void* stream);
+
+/*
+ * dK and dV of fused attention in one pass over queries: dv = sum_i p dout_i, dk = sum_i ds q_i.
+ * A hidden key gets zero rows. Replaces CUSTOM "sdpa_bwd_kv", reference
+ * limn/cuda_emit.py:1008-1083; numpy reference limn/sdpa.py:173-203.
+ */
+int limn_hip_sdpa_bwd_kv(const void* q, const void* k, const void* v, const void* dout, const void* lse, const void* delta,
+                         const void* key_mask, void* dk, void* dv, int dtype, int64_t batch, int64_t t_q, int64_t t_k,
+                         int64_t hd, int64_t hd_v, int causal, double scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LIMN_HIP_H */

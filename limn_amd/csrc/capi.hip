@@ -1,0 +1,122 @@
+// The C ABI declared in include/limn_hip.h: argument checks, kernel-family dispatch, errors.
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "sdpa.h"
+
+namespace limn {
+
+static thread_local char last_error[1024] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(last_error, sizeof last_error, fmt, ap);
+  va_end(ap);
+}
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(last_error, sizeof last_error, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_hip(hipError_t err, const char* doing) {
+  if (err == hipSuccess) return LIMN_HIP_OK;
+  return fail(LIMN_HIP_ERUNTIME, "hip: %s: %s", doing, hipGetErrorString(err));
+}
+
+static const char* pass_name(SdpaPass pass) {
+  return pass == SDPA_FWD ? "sdpa" : pass == SDPA_BWD_Q ? "sdpa_bwd_q" : "sdpa_bwd_kv";
+}
+
+// The same shape rules as the numpy reference's _validate (reference limn/sdpa.py:64-75),
+// on the flattened (batch, t, d) form the device hands over.
+static int validate(SdpaPass pass, const SdpaArgs& a) {
+  const char* name = pass_name(pass);
+  if (a.dtype < LIMN_HIP_FLOAT64 || a.dtype > LIMN_HIP_BFLOAT16)
+    return fail(LIMN_HIP_EUNSUPPORTED, "%s: dtype code %d is not a float dtype", name, a.dtype);
+  if (a.batch < 1 || a.t_q < 1 || a.t_k < 1 || a.hd < 1 || a.hd_v < 1)
+    return fail(LIMN_HIP_EINVAL, "%s: sizes must be positive (batch %lld, t_q %lld, t_k %lld, hd %lld, hd_v %lld)", name,
+                (long long)a.batch, (long long)a.t_q, (long long)a.t_k, (long long)a.hd, (long long)a.hd_v);
+  if (a.causal && a.t_q != a.t_k)
+    return fail(LIMN_HIP_EINVAL, "%s: causal attention needs square keys, got %lld queries and %lld keys", name,
+                (long long)a.t_q, (long long)a.t_k);
+  if (!isfinite(a.scale)) return fail(LIMN_HIP_EINVAL, "%s: scale must be finite", name);
+  if (a.q == nullptr || a.k == nullptr || a.v == nullptr || a.out0 == nullptr)
+    return fail(LIMN_HIP_EINVAL, "%s: null buffer", name);
+  if (pass == SDPA_FWD && a.out1 == nullptr) return fail(LIMN_HIP_EINVAL, "%s: null lse buffer", name);
+  if (pass != SDPA_FWD && (a.dout == nullptr || a.lse == nullptr || a.delta == nullptr))
+    return fail(LIMN_HIP_EINVAL, "%s: null dout/lse/delta buffer", name);
+  if (pass == SDPA_BWD_KV && a.out1 == nullptr) return fail(LIMN_HIP_EINVAL, "%s: null dv buffer", name);
+  const int64_t limit = (int64_t)1 << 40;  // element counts far past any allocation; keeps index math in range
+  if (a.t_q > limit / a.batch || a.t_k > limit / a.batch || a.hd > 4096 || a.hd_v > 4096)
+    return fail(LIMN_HIP_EUNSUPPORTED, "%s: sizes out of range", name);
+  return LIMN_HIP_OK;
+}
+
+static int run(SdpaPass pass, const SdpaArgs& a) {
+  const int rc = validate(pass, a);
+  if (rc != LIMN_HIP_OK) return rc;
+  if (mfma_supports(a.dtype, a.hd, a.hd_v)) return launch_sdpa_mfma(pass, a);
+  if (rows_supports(a.dtype, a.hd, a.hd_v)) return launch_sdpa_rows(pass, a);
+  return fail(LIMN_HIP_EUNSUPPORTED, "%s: no kernel for head dims %lld and %lld (at most 256)", pass_name(pass),
+              (long long)a.hd, (long long)a.hd_v);
+}
+
+}  // namespace limn
+
+using namespace limn;
+
+extern "C" {
+
+int limn_hip_abi_version(void) { return LIMN_HIP_ABI_VERSION; }
+
+const char* limn_hip_last_error(void) { return last_error; }
+
+int limn_hip_device_info(int device, char* arch, int arch_len, int* compute_units, int* clock_khz, int64_t* global_mem) {
+  hipDeviceProp_t prop;
+  const int rc = check_hip(hipGetDeviceProperties(&prop, device), "reading device properties");
+  if (rc != LIMN_HIP_OK) return rc;
+  if (arch != nullptr && arch_len > 0) snprintf(arch, (size_t)arch_len, "%s", prop.gcnArchName);
+  if (compute_units != nullptr) *compute_units = prop.multiProcessorCount;
+  if (clock_khz != nullptr) *clock_khz = prop.clockRate;
+  if (global_mem != nullptr) *global_mem = (int64_t)prop.totalGlobalMem;
+  return LIMN_HIP_OK;
+}
+
+int limn_hip_sdpa_path(int dtype, int64_t hd, int64_t hd_v) {
+  if (mfma_supports(dtype, hd, hd_v)) return 1;
+  if (rows_supports(dtype, hd, hd_v)) return 0;
+  return -1;
+}
+
+int limn_hip_sdpa_fwd(const void* q, const void* k, const void* v, const void* key_mask, void* out, void* lse, int dtype,
+                      int64_t batch, int64_t t_q, int64_t t_k, int64_t hd, int64_t hd_v, int causal, double scale,
+                      void* stream) {
+  SdpaArgs a = {q,     k,   v,    nullptr, nullptr, nullptr, key_mask, out,    lse,      dtype,
+                batch, t_q, t_k,  hd,      hd_v,    causal != 0, scale, (hipStream_t)stream};
+  return run(SDPA_FWD, a);
+}
+
+int limn_hip_sdpa_bwd_q(const void* q, const void* k, const void* v, const void* dout, const void* lse, const void* delta,
+                        const void* key_mask, void* dq, int dtype, int64_t batch, int64_t t_q, int64_t t_k, int64_t hd,
+                        int64_t hd_v, int causal, double scale, void* stream) {
+  SdpaArgs a = {q,     k,   v,   dout, lse,  delta,       key_mask, dq,   nullptr, dtype,
+                batch, t_q, t_k, hd,   hd_v, causal != 0, scale,    (hipStream_t)stream};
+  return run(SDPA_BWD_Q, a);
+}
+
+int limn_hip_sdpa_bwd_kv(const void* q, const void* k, const void* v, const void* dout, const void* lse, const void* delta,
+                         const void* key_mask, void* dk, void* dv, int dtype, int64_t batch, int64_t t_q, int64_t t_k,
+                         int64_t hd, int64_t hd_v, int causal, double scale, void* stream) {
+  SdpaArgs a = {q,     k,   v,   dout, lse,  delta,       key_mask, dk,   dv, dtype,
+                batch, t_q, t_k, hd,   hd_v, causal != 0, scale,    (hipStream_t)stream};
+  return run(SDPA_BWD_KV, a);
+}
+
+}  // extern "C"

@@ -1,0 +1,207 @@
+"""The `hip` device: limn's CompiledDevice on one MI355X (gfx950).
+
+It is what reference `limn/backend_cuda.py:272-415` (`CudaDevice`) is for NVIDIA, designed for
+this GPU rather than translated:
+
+- memory is hipMalloc'd device buffers recycled through a per-size pool (a training step
+  retires one output per kernel; hipMalloc/hipFree per call would dominate it);
+- lowered loop nests are rendered by limn_amd/hip/emit.py into gfx950 kernels, compiled by
+  hipRTC once per program and launched with hipModuleLaunchKernel on the null stream;
+- the CUSTOM attention kernels `sdpa`, `sdpa_bwd_q` and `sdpa_bwd_kv` are the hand-written
+  MFMA/LDS kernels of liblimn_hip.so, reached through its C ABI (include/limn_hip.h);
+- host arrays handed in are uploaded per batch (`prepare`), and an ASSIGN whose target is a host
+  array is written back (`commit`), as the reference device does;
+- `finish()` synchronizes once per batch, which pins an asynchronous failure to its batch.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+
+from limn_amd.codegen import LoopNest
+from limn_amd.dtypes import ABI_CODE
+from limn_amd.hip import runtime
+from limn_amd.hip.runtime import DEVICE_TO_DEVICE, DEVICE_TO_HOST, HOST_TO_DEVICE, check, check_limn
+from limn_amd.jit import Buffer, CompiledDevice, Runner
+from limn_amd.ops import FLOATS, Node, accumulate_in
+
+SDPA, SDPA_BWD_Q, SDPA_BWD_KV = "sdpa", "sdpa_bwd_q", "sdpa_bwd_kv"
+
+
+class HipBuffer:
+    """Device bytes; the pointer returns to its device's pool when the last reference drops."""
+
+    __slots__ = ("ptr", "nbytes", "pool")
+
+    def __init__(self, ptr: int, nbytes: int, pool: dict[int, list[int]]):
+        self.ptr = ptr
+        self.nbytes = nbytes
+        self.pool = pool
+
+    def __del__(self) -> None:
+        try:
+            self.pool.setdefault(self.nbytes, []).append(self.ptr)
+        except Exception:  # interpreter teardown
+            pass
+
+
+class HipDevice(CompiledDevice):
+    """Construct through set_device("hip"), which checks the runtime and the GPU first."""
+
+    def __init__(self) -> None:
+        super().__init__()
+        api = runtime.hip()
+        assert api is not None, "construct via set_device('hip'), which explains what is missing"
+        self.api = api
+        self.lib = runtime.kernels()
+        check(api.hipInit(0), "hipInit")
+        check(api.hipSetDevice(0), "selecting device 0")
+        arch = ctypes.create_string_buffer(256)
+        cus, clock = ctypes.c_int(), ctypes.c_int()
+        mem = ctypes.c_int64()
+        check_limn(self.lib.limn_hip_device_info(0, arch, 256, ctypes.byref(cus), ctypes.byref(clock), ctypes.byref(mem)))
+        self.arch = arch.value.decode()
+        self.compute_units = cus.value
+        self.clock_khz = clock.value
+        self.global_mem = mem.value
+        self.pool: dict[int, list[int]] = {}
+        self.custom[SDPA] = self._sdpa_runner
+        self.custom[SDPA_BWD_Q] = self._sdpa_runner
+        self.custom[SDPA_BWD_KV] = self._sdpa_runner
+
+    # ---- Device protocol ----
+
+    def _alloc(self, nb: int) -> HipBuffer:
+        free = self.pool.get(nb)
+        if free:
+            return HipBuffer(free.pop(), nb, self.pool)
+        ptr = ctypes.c_void_p()
+        status = self.api.hipMalloc(ctypes.byref(ptr), max(nb, 1))
+        if status != 0 and self.pool:
+            self.trim()
+            status = self.api.hipMalloc(ctypes.byref(ptr), max(nb, 1))
+        check(status, f"allocating {nb} bytes")
+        return HipBuffer(ptr.value, nb, self.pool)
+
+    def trim(self) -> None:
+        """Give every pooled buffer back to the runtime."""
+        self.finish()
+        for ptrs in self.pool.values():
+            for ptr in ptrs:
+                self.api.hipFree(ctypes.c_void_p(ptr))
+        self.pool.clear()
+
+    def alloc(self, nbytes: int) -> Buffer:
+        return self.out_alloc(nbytes, zero=True)
+
+    def copyin(self, buf: Buffer, array: np.ndarray) -> None:
+        data = np.ascontiguousarray(array)
+        if data.nbytes != buf.nbytes:
+            raise ValueError(f"copyin: {data.nbytes} bytes into a {buf.nbytes}-byte buffer")
+        check(self.api.hipMemcpy(ctypes.c_void_p(buf.ptr), data.ctypes.data_as(ctypes.c_void_p), data.nbytes, HOST_TO_DEVICE), "uploading bytes")
+
+    def copyout(self, buf: Buffer) -> np.ndarray:
+        out = np.empty(buf.nbytes, dtype=np.uint8)
+        check(self.api.hipMemcpy(out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(buf.ptr), buf.nbytes, DEVICE_TO_HOST), "downloading bytes")
+        return out
+
+    # ---- CompiledDevice hooks ----
+
+    def prepare(self, buf: Buffer) -> Buffer:
+        if isinstance(buf, np.ndarray):  # a tensor whose bytes live on the host
+            moved = self._alloc(buf.nbytes)
+            self.copyin(moved, buf)
+            return moved
+        return buf
+
+    def out_alloc(self, nb: int, zero: bool) -> Buffer:
+        buf = self._alloc(nb)
+        if zero:
+            check(self.api.hipMemsetAsync(ctypes.c_void_p(buf.ptr), 0, nb, None), "zeroing an allocation")
+        return buf
+
+    def commit(self, target: Buffer, value: Buffer) -> None:
+        if isinstance(target, np.ndarray):
+            check(self.api.hipMemcpy(target.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(value.ptr), target.nbytes, DEVICE_TO_HOST), "committing an assign to host")
+        else:
+            check(self.api.hipMemcpyAsync(ctypes.c_void_p(target.ptr), ctypes.c_void_p(value.ptr), value.nbytes, DEVICE_TO_DEVICE, None), "committing an assign")
+
+    def finish(self) -> None:
+        check(self.api.hipDeviceSynchronize(), "waiting for the batch")
+
+    def runners(self, nests: list[LoopNest]) -> list[Runner]:
+        from limn_amd.hip.emit import nest_runners
+
+        return nest_runners(self, nests)
+
+    # ---- fused attention ----
+
+    def _sdpa_runner(self, node: Node) -> Runner:
+        """The three CUSTOM attention kernels, bound to liblimn_hip.so's entry points.
+
+        srcs are (q, k, v[, mask]) for the forward and (q, k, v, dout, lse, delta[, mask]) for
+        both backward passes, contiguous, with shared leading (batch) dims; a mask rides last
+        (reference `limn/tensor.py:562-567, 707-712`). Shapes are checked here, at plan time.
+        """
+        name = node.arg.name
+        causal, scale = node.arg.params
+        q, k, v = node.srcs[:3]
+        base = 3 if name == SDPA else 6
+        masked = len(node.srcs) == base + 1
+        if len(node.srcs) not in (base, base + 1):
+            raise ValueError(f"{name}: expected {base} or {base + 1} srcs, got {len(node.srcs)}")
+        dtype = q.dtype
+        if dtype not in FLOATS or dtype not in ABI_CODE:
+            raise NotImplementedError(f"{name}: no kernel for dtype {dtype}")
+        if any(s.dtype != dtype for s in (k, v)) or (masked and node.srcs[-1].dtype != dtype):
+            raise ValueError(f"{name}: q, k, v and the mask must share a dtype")
+        if len(q.shape) < 2 or len(k.shape) != len(q.shape) or len(v.shape) != len(q.shape):
+            raise ValueError(f"{name} wants 2D+ inputs of equal rank, got {q.shape}, {k.shape}, {v.shape}")
+        lead = q.shape[:-2]
+        if k.shape[:-2] != lead or v.shape[:-2] != lead or k.shape[-2] != v.shape[-2] or q.shape[-1] != k.shape[-1]:
+            raise ValueError(f"{name} shape mismatch: {q.shape}, {k.shape}, {v.shape}")
+        batch, t_q, hd = math.prod(lead), q.shape[-2], q.shape[-1]
+        t_k, hd_v = k.shape[-2], v.shape[-1]
+        if causal and t_q != t_k:
+            raise ValueError(f"causal {name} needs square keys, got {t_q} queries and {t_k} keys")
+        if masked and node.srcs[-1].shape != lead + (t_k,):
+            raise ValueError(f"{name} key mask must be {lead + (t_k,)}, got {node.srcs[-1].shape}")
+        if name != SDPA:
+            stat = accumulate_in(dtype)
+            do, lse, delta = node.srcs[3:6]
+            if do.shape != lead + (t_q, hd_v) or do.dtype != dtype:
+                raise ValueError(f"{name}: dout must be {lead + (t_q, hd_v)} {dtype}, got {do.shape} {do.dtype}")
+            for stat_node, what in ((lse, "lse"), (delta, "delta")):
+                if stat_node.dtype != stat or math.prod(stat_node.shape) != batch * t_q:
+                    raise ValueError(f"{name}: {what} must hold {batch * t_q} {stat} values")
+        code = ABI_CODE[dtype]
+        if self.lib.limn_hip_sdpa_path(code, hd, hd_v) < 0:
+            raise NotImplementedError(f"{name}: no kernel for head dims {hd} and {hd_v}")
+        lib, sizes = self.lib, (batch, t_q, t_k, hd, hd_v, int(bool(causal)), float(scale), None)
+
+        if name == SDPA:
+
+            def run(inputs: list[Buffer], outs: list[Buffer]) -> None:
+                mask = inputs[3].ptr if masked else None
+                check_limn(lib.limn_hip_sdpa_fwd(inputs[0].ptr, inputs[1].ptr, inputs[2].ptr, mask, outs[0].ptr, outs[1].ptr, code, *sizes))
+
+        elif name == SDPA_BWD_Q:
+
+            def run(inputs: list[Buffer], outs: list[Buffer]) -> None:
+                mask = inputs[6].ptr if masked else None
+                ptrs = [b.ptr for b in inputs[:6]]
+                check_limn(lib.limn_hip_sdpa_bwd_q(*ptrs, mask, outs[0].ptr, code, *sizes))
+
+        elif name == SDPA_BWD_KV:
+
+            def run(inputs: list[Buffer], outs: list[Buffer]) -> None:
+                mask = inputs[6].ptr if masked else None
+                ptrs = [b.ptr for b in inputs[:6]]
+                check_limn(lib.limn_hip_sdpa_bwd_kv(*ptrs, mask, outs[0].ptr, outs[1].ptr, code, *sizes))
+
+        else:
+            raise NotImplementedError(f"HipDevice has no kernel for custom op {name!r}")
+        return run

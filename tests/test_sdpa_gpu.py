@@ -1,0 +1,207 @@
+"""Fused attention on the MI355X: the three CUSTOM kernels (sdpa, sdpa_bwd_q, sdpa_bwd_kv) run
+through the hip device's CompiledDevice boundary and its C ABI, diffed against the oracle on the
+same inputs.
+
+Tolerances are the reference's own for its GPU device against the numpy reference
+(tests/test_attention.py:250-308 there): forward f32 1e-5, f16 2e-3, bf16 1e-2; backward f32
+1e-4, f16 4e-3, bf16 3e-2, as rtol = atol (its conftest.check). Each kernel gets the same
+inputs on both sides (the GPU forward's L and delta feed both backward checks), so a failure
+names one kernel.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from conftest import DTYPES, download, storage_values, upload
+from limn_amd.ops import accumulate_in, custom
+from oracle import sdpa as ref
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+FWD_TOL = {"float64": 1e-12, "float32": 1e-5, "float16": 2e-3, "bfloat16": 1e-2}
+BWD_TOL = {"float64": 1e-11, "float32": 1e-4, "float16": 4e-3, "bfloat16": 3e-2}
+
+
+def forward(dev, q, k, v, mask, causal, dtype_name):
+    dtype = DTYPES[dtype_name]
+    scale = q.shape[-1] ** -0.5
+    srcs = [upload(dev, x, dtype) for x in (q, k, v)]
+    if mask is not None:
+        srcs.append(upload(dev, mask, dtype))
+    lead, t_q = q.shape[:-2], q.shape[-2]
+    outs = ((dtype, lead + (t_q, v.shape[-1])), (accumulate_in(dtype), lead + (t_q, 1)))
+    o, lse = custom("sdpa", tuple(srcs), (causal, scale), outs)
+    bo, bl = dev.execute([o, lse])
+    return download(dev, bo, dtype, o.shape), download(dev, bl, accumulate_in(dtype), lse.shape)
+
+
+def backward(dev, q, k, v, do, lse, delta, mask, causal, dtype_name):
+    dtype = DTYPES[dtype_name]
+    stat = accumulate_in(dtype)
+    scale = q.shape[-1] ** -0.5
+    srcs = [upload(dev, x, dtype) for x in (q, k, v, do)] + [upload(dev, lse, stat), upload(dev, delta, stat)]
+    if mask is not None:
+        srcs.append(upload(dev, mask, dtype))
+    (dq,) = custom("sdpa_bwd_q", tuple(srcs), (causal, scale), ((dtype, q.shape),))
+    dk, dv = custom("sdpa_bwd_kv", tuple(srcs), (causal, scale), ((dtype, k.shape), (dtype, v.shape)))
+    bufs = dev.execute([dq, dk, dv])
+    return [download(dev, b, dtype, n.shape) for b, n in zip(bufs, (dq, dk, dv))]
+
+
+def draw(seed, q_shape, k_shape, v_shape, dtype_name, live=None):
+    rng = np.random.default_rng(seed)
+    dtype = DTYPES[dtype_name]
+    q, k, v = (storage_values(rng.standard_normal(s).astype(np.float32), dtype) for s in (q_shape, k_shape, v_shape))
+    do = storage_values(rng.standard_normal(q_shape[:-1] + v_shape[-1:]).astype(np.float32), dtype)
+    mask = None
+    if live is not None:
+        mask = np.broadcast_to(np.arange(k_shape[-2]) < live, k_shape[:-1]).astype(np.float32)
+    if dtype_name == "float64":
+        q, k, v, do = (x.astype(np.float64) for x in (q, k, v, do))
+        mask = None if mask is None else mask.astype(np.float64)
+    return q, k, v, do, mask
+
+
+def check_case(dev, seed, shapes, causal, dtype_name, live=None):
+    q, k, v, do, mask = draw(seed, *shapes, dtype_name, live)
+    scale = q.shape[-1] ** -0.5
+    out, lse = forward(dev, q, k, v, mask, causal, dtype_name)
+    want_out, want_lse = ref.sdpa(q, k, v, mask, causal=causal, scale=scale, dtype=dtype_name)
+    tol = FWD_TOL[dtype_name]
+    np.testing.assert_allclose(out, want_out, rtol=tol, atol=tol)
+    np.testing.assert_allclose(lse, want_lse, rtol=tol, atol=tol)
+    delta = (do.astype(np.float64) * out).sum(axis=-1, keepdims=True).astype(lse.dtype)
+    dq, dk, dv = backward(dev, q, k, v, do, lse, delta, mask, causal, dtype_name)
+    args = (q, k, v, do, lse, delta, mask)
+    want_dq = ref.sdpa_backward_q(*args, causal=causal, scale=scale, dtype=dtype_name)
+    want_dk, want_dv = ref.sdpa_backward_kv(*args, causal=causal, scale=scale, dtype=dtype_name)
+    tol = BWD_TOL[dtype_name]
+    for name, got, want in (("dq", dq, want_dq), ("dk", dk, want_dk), ("dv", dv, want_dv)):
+        np.testing.assert_allclose(got, want, rtol=tol, atol=tol, err_msg=name)
+    return out, lse, dq, dk, dv
+
+
+# general-width family: the shapes of the reference's own GPU attention tests
+ROWS_CASES = {
+    "batched": ((2, 3, 64, 16), (2, 3, 64, 16), (2, 3, 64, 24)),
+    "ragged": ((2, 2, 100, 16), (2, 2, 100, 16), (2, 2, 100, 24)),
+    "several_chunks": ((300, 16), (300, 16), (300, 24)),
+}
+
+
+@pytest.mark.parametrize("dtype_name", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("case", sorted(ROWS_CASES))
+def test_rows_family_matches_the_oracle(hipdev, case, causal, dtype_name):
+    check_case(hipdev, 1, ROWS_CASES[case], causal, dtype_name)
+
+
+def test_rows_family_rectangular_keys(hipdev):
+    check_case(hipdev, 2, ((40, 8), (72, 8), (72, 12)), False, "float32")
+
+
+def test_rows_family_float64(hipdev):
+    check_case(hipdev, 3, ((2, 64, 32), (2, 64, 32), (2, 64, 16)), True, "float64")
+
+
+@pytest.mark.parametrize(
+    "shapes,causal,live",
+    [(((2, 100, 16), (2, 100, 16), (2, 100, 16)), True, 66), (((4, 1, 32), (4, 96, 32), (4, 96, 48)), False, 64)],
+    ids=["ragged_causal", "decode_row"],
+)
+def test_rows_family_key_mask(hipdev, shapes, causal, live):
+    _, _, _, dk, dv = check_case(hipdev, 4, shapes, causal, "float32", live)
+    assert (dk[..., live:, :] == 0).all() and (dv[..., live:, :] == 0).all()
+
+
+# MFMA family: bf16/f16 at D = 64 and 128
+MFMA_CASES = {
+    "d64_ragged": ((2, 2, 200, 64), (2, 2, 200, 64), (2, 2, 200, 64)),
+    "d128_two_blocks": ((1, 2, 256, 128), (1, 2, 256, 128), (1, 2, 256, 128)),
+    "d128_ragged": ((2, 1, 333, 128), (2, 1, 333, 128), (2, 1, 333, 128)),
+}
+
+
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float16"])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("case", sorted(MFMA_CASES))
+def test_mfma_family_matches_the_oracle(hipdev, case, causal, dtype_name):
+    check_case(hipdev, 5, MFMA_CASES[case], causal, dtype_name)
+
+
+def test_mfma_family_rectangular_keys(hipdev):
+    check_case(hipdev, 6, ((3, 70, 64), (3, 190, 64), (3, 190, 64)), False, "bfloat16")
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_mfma_family_key_mask(hipdev, causal):
+    shapes = ((2, 150, 128), (2, 150, 128), (2, 150, 128))
+    _, _, _, dk, dv = check_case(hipdev, 7, shapes, causal, "bfloat16", live=97)
+    assert (dk[..., 97:, :] == 0).all() and (dv[..., 97:, :] == 0).all()
+
+
+@pytest.mark.parametrize("dtype_name,hd", [("bfloat16", 128), ("float32", 64)])
+def test_same_bits_twice(hipdev, dtype_name, hd):
+    """Every total is owned by one wave and folded in a fixed order: no atomics, same bits."""
+    q, k, v, do, _ = draw(8, (2, 2, 300, hd), (2, 2, 300, hd), (2, 2, 300, hd), dtype_name)
+    first = forward(hipdev, q, k, v, None, True, dtype_name)
+    second = forward(hipdev, q, k, v, None, True, dtype_name)
+    for a, b in zip(first, second):
+        np.testing.assert_array_equal(a, b)
+    out, lse = first
+    delta = (do * out).sum(axis=-1, keepdims=True).astype(lse.dtype)
+    g1 = backward(hipdev, q, k, v, do, lse, delta, None, True, dtype_name)
+    g2 = backward(hipdev, q, k, v, do, lse, delta, None, True, dtype_name)
+    for a, b in zip(g1, g2):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_config1_matches_torch_golden(hipdev):
+    """BASELINE config 1 end to end: f32 causal B=2 H=4 S=256 D=64 from seed 1, forward and
+    backward (delta from the GPU forward), against torch's float64 answer."""
+    rng = np.random.default_rng(1)
+    shape = (2, 4, 256, 64)
+    q, k, v, do = (rng.standard_normal(shape, dtype=np.float32) for _ in range(4))
+    out, lse = forward(hipdev, q, k, v, None, True, "float32")
+    delta = (do * out).sum(axis=-1, keepdims=True)
+    dq, dk, dv = backward(hipdev, q, k, v, do, lse, delta, None, True, "float32")
+    g = np.load(GOLDEN / "config1_sdpa.npz")
+    for key, val, tol in (("o", out, 1e-5), ("lse", lse, 1e-5), ("dq", dq, 1e-4), ("dk", dk, 1e-4), ("dv", dv, 1e-4)):
+        assert ref.worst(val[0, 0], g[f"{key}_slice"]) <= tol, key
+        np.testing.assert_allclose(float((val.astype(np.float64) ** 2).sum()), float(g[f"{key}_sumsq"]), rtol=1e-4)
+
+
+def test_config4_full_size_two_heads(hipdev):
+    """BASELINE config 4 at its full shape (bf16, causal, B=8 H=16 S=4096 D=128, seed 4):
+    the GPU runs all 128 heads; heads are independent, so two of them (the first and the last)
+    are diffed against the oracle, and every output must be finite."""
+    B, H, S, D = 8, 16, 4096, 128
+    rng = np.random.default_rng(4)
+    from limn_amd.dtypes import bf16_bits, bf16_values
+
+    def rnd():
+        return bf16_values(bf16_bits(rng.standard_normal((B, H, S, D), dtype=np.float32)))
+
+    q, k, v, do = rnd(), rnd(), rnd(), rnd()
+    out, lse = forward(hipdev, q, k, v, None, True, "bfloat16")
+    assert np.isfinite(out).all() and np.isfinite(lse).all()
+    delta = (do * out).sum(axis=-1, keepdims=True).astype(np.float32)
+    dq, dk, dv = backward(hipdev, q, k, v, do, lse, delta, None, True, "bfloat16")
+    for g in (dq, dk, dv):
+        assert np.isfinite(g).all()
+    scale = D**-0.5
+    for b, h in ((0, 0), (B - 1, H - 1)):
+        args = [x[b, h] for x in (q, k, v)]
+        want_out, want_lse = ref.sdpa(*args, causal=True, scale=scale, dtype="bfloat16", block_size=256)
+        np.testing.assert_allclose(out[b, h], want_out, rtol=1e-2, atol=1e-2)
+        np.testing.assert_allclose(lse[b, h], want_lse, rtol=1e-2, atol=1e-2)
+        bargs = (*args, do[b, h], lse[b, h], delta[b, h])
+        want_dq = ref.sdpa_backward_q(*bargs, causal=True, scale=scale, dtype="bfloat16", block_size=256)
+        want_dk, want_dv = ref.sdpa_backward_kv(*bargs, causal=True, scale=scale, dtype="bfloat16", block_size=256)
+        for got, want in ((dq[b, h], want_dq), (dk[b, h], want_dk), (dv[b, h], want_dv)):
+            np.testing.assert_allclose(got, want, rtol=3e-2, atol=3e-2)
