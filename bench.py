@@ -40,7 +40,48 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument(
+        "--workload",
+        default="c4",
+        choices=["c4", "copy"],
+        help="c4: the headline attention step; copy: a plain 256 MiB device copy kernel, the "
+        "known-size reference that scales rocprofv3's FETCH_SIZE/WRITE_SIZE counters",
+    )
     return p.parse_args()
+
+
+COPY_SOURCE = """
+extern "C" __global__ void limn_copy_probe(const float4* __restrict__ src, float4* __restrict__ dst, long long n) {
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+"""
+
+
+def copy_probe(steps: int) -> int:
+    """A grid-stride float4 copy of 256 MiB, `steps` times: 268435456 bytes read and written per
+    launch. Prints its own JSON line (not a bench line) with the measured bandwidth."""
+    from limn_amd.hip import runtime
+    from limn_amd.hip.device import HipDevice
+
+    dev = HipDevice()
+    nbytes = 256 << 20
+    src, dst = dev.out_alloc(nbytes, True), dev.out_alloc(nbytes, True)
+    fn = runtime.load_functions(COPY_SOURCE, ["limn_copy_probe"])["limn_copy_probe"]
+    n = ctypes.c_longlong(nbytes // 16)
+    a, b = ctypes.c_void_p(src.ptr), ctypes.c_void_p(dst.ptr)
+    params = (ctypes.c_void_p * 3)(ctypes.addressof(a), ctypes.addressof(b), ctypes.addressof(n))
+    ev = Events(dev.api, 2)
+    for i in range(steps + 1):
+        if i == 1:
+            ev.record(0)
+        runtime.check(dev.api.hipModuleLaunchKernel(fn, 4096, 1, 1, 256, 1, 1, 0, None, params, None), "launching the copy")
+    ev.record(1)
+    dev.finish()
+    ms = ev.ms(0, 1) / steps
+    print(json.dumps({"probe": "copy", "bytes_read": nbytes, "bytes_written": nbytes, "ms": round(ms, 4),
+                      "GB_s": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+    return 0
 
 
 class Events:
@@ -100,6 +141,8 @@ def main() -> int:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (every box has one MI355X)", file=sys.stderr)
         return 2
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    if args.workload == "copy":
+        return copy_probe(args.steps)
     from limn_amd.dtypes import bf16_bits, bf16_values
     from limn_amd.hip.device import HipDevice
     from limn_amd.hip.runtime import hip_unavailable
