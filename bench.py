@@ -43,7 +43,7 @@ def parse() -> argparse.Namespace:
     p.add_argument(
         "--workload",
         default="c4",
-        choices=["c4", "copy"],
+        choices=["c4", "copy", "c2"],
         help="c4: the headline attention step; copy: a plain 256 MiB device copy kernel, the "
         "known-size reference that scales rocprofv3's FETCH_SIZE/WRITE_SIZE counters",
     )
@@ -135,6 +135,101 @@ def cpu_baseline(q, k, v, do, scale: float, B: int, H: int, units: float) -> dic
     }
 
 
+def record_plan(dev, sinks):
+    """Run a graph once through the device and return the plan and bound buffers it used."""
+    dev.record = []
+    dev.execute(sinks)
+    rec = dev.record[0]
+    dev.record = None
+    return rec.plan, dict(zip(rec.plan.buffers, rec.bound))
+
+
+def timed_calls(dev, plan, sources, ev: Events, base: int) -> int:
+    """The plan's calls exactly as CompiledDevice.run issues them (fresh pooled outputs, inputs
+    by position), with an event before each call and after the last. Returns the next free
+    event index."""
+    bufs = [None] * plan.positions
+    for p, buf in sources.items():
+        bufs[p] = dev.prepare(buf)
+    for i, call in enumerate(plan.calls):
+        outs = [dev.out_alloc(nb, call.zero_fill) for nb in call.out_nbytes]
+        ev.record(base + i)
+        call.fn([bufs[p] for p in call.inputs], outs)
+        for p, out in zip(call.outputs, outs):
+            if p is not None:
+                bufs[p] = out
+    ev.record(base + len(plan.calls))
+    return base + len(plan.calls) + 1
+
+
+def bench_c2(dev, steps: int, warmup: int) -> dict:
+    """x f32 (8192, 8192) ~ N(0,1) from default_rng(2); row softmax then
+    LayerNorm (gamma 1, beta 0, eps 1e-5), fused by the scheduler into its 11 kernels and
+    emitted by the hip device. Reports the chain's algorithmic GB/s and each kernel's."""
+    from limn_amd import device as limn_device
+    from limn_amd.tensor import Tensor
+
+    N = 8192
+    limn_device.active_device = dev
+    x = Tensor(np.random.default_rng(2).standard_normal((N, N), dtype=np.float32))
+    w, b = Tensor.ones((N,)), Tensor.zeros((N,))
+    y = x.softmax(-1)
+    c = y - y.mean(axis=-1, keepdim=True)
+    var = (c * c).mean(axis=-1, keepdim=True)
+    out = c / (var + 1e-5).sqrt() * w + b
+    plan, sources = record_plan(dev, [out.node])
+    ncalls = len(plan.calls)
+    for _ in range(warmup):
+        timed_calls(dev, plan, sources, Events(dev.api, ncalls + 1), 0)
+    dev.finish()
+    ev = Events(dev.api, steps * (ncalls + 1))
+    for s_ in range(steps):
+        timed_calls(dev, plan, sources, ev, s_ * (ncalls + 1))
+    dev.finish()
+    per = np.zeros(ncalls)
+    for s_ in range(steps):
+        base = s_ * (ncalls + 1)
+        per += [ev.ms(base + i, base + i + 1) for i in range(ncalls)]
+    per /= steps
+    chain_ms = float(per.sum())
+    # algorithmic bytes per kernel: every input read once plus the output written once
+    kernels = []
+    # input bytes come from the recorded plan's positions: a position's bytes are its output size
+    # (computed values) or its bound buffer's size (BUFFER inputs)
+    pos_bytes = {}
+    for call in plan.calls:
+        for p, nb in zip(call.outputs, call.out_nbytes):
+            if p is not None:
+                pos_bytes[p] = nb
+    for p, buf in sources.items():
+        pos_bytes[p] = buf.nbytes if hasattr(buf, "nbytes") else 0
+    total = 0
+    for i, call in enumerate(plan.calls):
+        moved = sum(pos_bytes.get(p, 0) for p in call.inputs) + sum(call.out_nbytes)
+        total += moved
+        kernels.append({"ms": round(float(per[i]), 4), "bytes": moved, "GB_s": round(moved / (per[i] * 1e-3) / 1e9, 1)})
+    dom = int(np.argmax(per))
+    achieved = kernels[dom]["bytes"] / (per[dom] * 1e-3)
+    return {
+        "metric": "fused-kernel HBM GB/s",
+        "value": round(total / (chain_ms * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "ms_per_step": round(chain_ms, 4),
+        "dtype": "f32",
+        "config": {"workload": "C2 row softmax -> LayerNorm, x f32 (8192, 8192), 11 scheduled kernels", "bytes_per_step": total},
+        "kernels": kernels,
+        "roofline": {
+            "kernel": f"k{dom}",
+            "bound": "hbm",
+            "achieved": round(achieved / 1e9, 1),
+            "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK, 4),
+            "traffic": None,
+        },
+    }
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -143,6 +238,11 @@ def main() -> int:
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     if args.workload == "copy":
         return copy_probe(args.steps)
+    if args.workload == "c2":
+        from limn_amd.hip.device import HipDevice
+
+        print(json.dumps(bench_c2(HipDevice(), args.steps, args.warmup)), flush=True)
+        return 0
     from limn_amd.dtypes import bf16_bits, bf16_values
     from limn_amd.hip.device import HipDevice
     from limn_amd.hip.runtime import hip_unavailable
@@ -254,6 +354,8 @@ def main() -> int:
     if not args.no_cpu:
         inputs = [bf16_values(h.reshape(B, H, S, D)[:1, :1]) for h in host]
         line["cpu_baseline"] = cpu_baseline(*inputs, scale, B, H, step_flops)
+    del q, k, v, do, out, lse, dq, dk, dv, delta, lse_node, o_node, l_node, dq_node, dk_node
+    line["workloads"] = {"C2": bench_c2(dev, args.steps, args.warmup)}
     print(json.dumps(line), flush=True)
     return 0
 

@@ -230,9 +230,9 @@ def lower(kernel: Kernel, name: str) -> LoopNest:
 
     order = loop_order(kernel, len(space), axes)
     outer = tuple(d for d in order if d not in axes)
-    out_index = contiguous_index(kernel.target.shape, loop_vars)
 
     if axes and order[-1] not in axes:
+        out_index = contiguous_index(kernel.target.shape, loop_vars)
         reduce = REDUCES[root.op]
         open_(outer)
         start = emit(Opcode.CONST, root.dtype, arg=(reduce.identity[root.dtype], Valid()))
@@ -266,6 +266,7 @@ def lower(kernel: Kernel, name: str) -> LoopNest:
     if root.op is Op.SCATTER:
         instrs.append(Instr(Opcode.SCATTER, dtype=root.dtype, srcs=(result,), arg=("out", row_index(root.shape, root.srcs[0]))))
     else:
+        out_index = contiguous_index(kernel.target.shape, loop_vars)
         instrs.append(Instr(Opcode.STORE, dtype=root.dtype, srcs=(result,), arg=("out", out_index)))
     close(outer)
     return LoopNest(name, kernel, tuple(space), tuple(instrs))

@@ -1,0 +1,563 @@
+"""The HIP emitter: limn's loop-nest IR (limn_amd/codegen.py) rendered as gfx950 kernels.
+
+One hipRTC program per plan holds every nest's kernel; `nest_runners` compiles it (cached by
+source hash) and returns one launcher per nest, in order, which is the `runners()` contract of
+reference `limn/jit.py:113-115`. Semantics follow the reference's compiled backends
+(limn/backend_c.py:54-143, limn/cuda_emit.py:45-373, 688-733): masked reads are 0, half widths
+compute in float and round to nearest even on store, a CAST to a half width rounds, MAX
+propagates NaN, narrow ints wrap, reduces total at `accumulate_in` width.
+
+How each nest maps onto the GPU (designed for wave64 CDNA4, not the reference's
+one-thread-per-cell launch):
+
+- no reduce (elementwise, CONTIGUOUS, ASSIGN, GATHER, SCATTER): a grid-stride loop over output
+  cells, VEC consecutive cells of the innermost (stride-1) dim per thread so a wave's loads and
+  stores cover contiguous 16-byte runs;
+- a reduce is `cells x reduce-space` whatever form the IR gave it (register ACC/UPDATE or
+  in-place ACCUM). GROUP threads own a cell: 1 (a thread per cell, for short reduces and for the
+  ACCUM form whose kept dim is the stride-1 one, so neighbouring threads read neighbouring
+  columns), 64 (a wave per cell) or 256 (a workgroup per cell, for long rows: lanes stride
+  through the row with VEC-wide runs, then a fixed butterfly across the wave and a fixed fold
+  across waves in LDS). Every cell's total is formed in one fixed order, so reruns give the
+  same bits;
+- few cells over a long reduce (the reference's split reduce, limn/cuda_emit.py:134-149):
+  PARTS workgroups per cell write partials to a scratch buffer, and a second kernel folds each
+  cell's partials in index order;
+- SCATTER adds with hardware atomics (float32, float64, int32); like the reference's GPU
+  device, the half widths and narrow ints are refused.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from limn_amd.codegen import Index, Instr, LoopNest, Opcode, Valid
+from limn_amd.hip import runtime
+from limn_amd.ops import DType, Op, accumulate_in, bfloat16, float16, float32, float64, int8, int16, int32
+
+THREADS = 256
+
+STORE_T = {float64: "double", float32: "float", float16: "unsigned short", bfloat16: "unsigned short", int32: "int", int16: "short", int8: "signed char"}
+VALUE_T = {float64: "double", float32: "float", float16: "float", bfloat16: "float", int32: "int", int16: "short", int8: "signed char"}
+HALVES = (float16, bfloat16)
+INTS = (int32, int16, int8)
+
+PRELUDE = r"""
+typedef long long i64;
+__device__ __forceinline__ float b2f(unsigned short b) { return __uint_as_float(((unsigned)b) << 16); }
+__device__ __forceinline__ unsigned short f2b(float x) { __bf16 h = (__bf16)x; return __builtin_bit_cast(unsigned short, h); }
+__device__ __forceinline__ float h2f(unsigned short b) { return (float)__builtin_bit_cast(_Float16, b); }
+__device__ __forceinline__ unsigned short f2h(float x) { return __builtin_bit_cast(unsigned short, (_Float16)x); }
+template <typename T> __device__ __forceinline__ T fmax_nan(T a, T b) { return (a > b || a != a) ? a : b; }
+template <typename T> __device__ __forceinline__ T fadd(T a, T b) { return a + b; }
+__device__ __forceinline__ int fadd(int a, int b) { return (int)((unsigned)a + (unsigned)b); }
+__device__ __forceinline__ short fadd(short a, short b) { return (short)(a + b); }
+__device__ __forceinline__ signed char fadd(signed char a, signed char b) { return (signed char)(a + b); }
+template <typename T> __device__ __forceinline__ T wave_fold_add(T x) {
+  for (int s = 32; s > 0; s >>= 1) x = fadd(x, (T)__shfl_xor(x, s));
+  return x;
+}
+template <typename T> __device__ __forceinline__ T wave_fold_max(T x) {
+  for (int s = 32; s > 0; s >>= 1) x = fmax_nan(x, (T)__shfl_xor(x, s));
+  return x;
+}
+"""
+
+
+def literal(value: float | int, dtype: DType) -> str:
+    """A scalar as a literal of the dtype's compute type (a half-width literal is the float it
+    rounds to)."""
+    if dtype in INTS:
+        v = int(value)
+        bits = 8 * dtype.itemsize
+        v = ((v + (1 << (bits - 1))) % (1 << bits)) - (1 << (bits - 1))
+        if v == -(1 << 31):
+            return "(-2147483647 - 1)"
+        return f"({VALUE_T[dtype]})({v})"
+    v = float(value)
+    if dtype is float16:
+        v = float(np.float16(v))
+    elif dtype is bfloat16:
+        from limn_amd.dtypes import bf16_bits, bf16_values
+
+        v = float(bf16_values(bf16_bits(np.array([v], dtype=np.float32)))[0])
+    if math.isnan(v):
+        return "__builtin_nan(\"\")" if dtype is float64 else "__builtin_nanf(\"\")"
+    if math.isinf(v):
+        s = "-" if v < 0 else ""
+        return f"({s}__builtin_inf())" if dtype is float64 else f"({s}__builtin_inff())"
+    if dtype is float64:
+        return repr(v)
+    f = float(np.float32(v))
+    if math.isinf(f):  # a finite double past float32's range
+        return "(-__builtin_inff())" if f < 0 else "(__builtin_inff())"
+    return repr(f) + "f"
+
+
+def load_expr(dtype: DType, ref: str) -> str:
+    if dtype is bfloat16:
+        return f"b2f({ref})"
+    if dtype is float16:
+        return f"h2f({ref})"
+    return ref
+
+
+def store_expr(dtype: DType, value: str) -> str:
+    if dtype is bfloat16:
+        return f"f2b({value})"
+    if dtype is float16:
+        return f"f2h({value})"
+    return f"({STORE_T[dtype]})({value})"
+
+
+def arith(op: Op, srcs: tuple[str, ...], dtype: DType) -> str:
+    t = VALUE_T[dtype]
+    wide = dtype is float64
+    if op is Op.NEG:
+        return f"({t})(-{srcs[0]})"
+    if op is Op.EXP:
+        return f"{'exp' if wide else 'expf'}({srcs[0]})"
+    if op is Op.LOG:
+        return f"{'log' if wide else 'logf'}({srcs[0]})"
+    if op is Op.SQRT:
+        return f"{'sqrt' if wide else 'sqrtf'}({srcs[0]})"
+    if op is Op.RECIP:
+        return f"({'1.0' if wide else '1.0f'} / {srcs[0]})"
+    if op is Op.ADD:
+        return f"fadd(({t}){srcs[0]}, ({t}){srcs[1]})" if dtype in INTS else f"({srcs[0]} + {srcs[1]})"
+    if op is Op.MUL:
+        if dtype is int32:
+            return f"(int)((unsigned){srcs[0]} * (unsigned){srcs[1]})"
+        return f"({t})({srcs[0]} * {srcs[1]})"
+    if op is Op.CMPLT:
+        return f"({t})({srcs[0]} < {srcs[1]})"
+    if op is Op.WHERE:
+        return f"(({srcs[0]}) != 0 ? ({srcs[1]}) : ({srcs[2]}))"
+    raise NotImplementedError(f"no HIP lowering for {op}")
+
+
+@dataclass
+class Buffers:
+    """Element types of a nest's buffers by name (in0.., out) and whether 64-bit indexing is needed."""
+
+    dtypes: dict[str, DType]
+    wide_index: bool
+
+
+def render_index(index: Index, wide: bool) -> str:
+    if not index.terms:
+        return str(index.const)
+    cast = "(i64)" if wide else ""
+    parts = [f"{cast}{var}" if c == 1 else f"{cast}{var} * {c}" for var, c in index.terms]
+    text = " + ".join(parts)
+    if index.const:
+        text += f" + {index.const}" if index.const > 0 else f" - {-index.const}"
+    return text
+
+
+def value_line(instr: Instr, bufs: Buffers) -> str:
+    """One value-defining instruction as a declaration."""
+    t = VALUE_T[instr.value_type]
+    op = instr.opcode
+    if op is Opcode.CONST:
+        value, valid = instr.arg
+        lit = literal(value, instr.value_type)
+        if valid.bounds:
+            return f"const {t} {instr.dest} = ({valid.render()}) ? {lit} : ({t})0;"
+        return f"const {t} {instr.dest} = {lit};"
+    if op is Opcode.LOAD:
+        buf, index, valid = instr.arg
+        ref = load_expr(bufs.dtypes[buf], f"{buf}[{render_index(index, bufs.wide_index)}]")
+        if valid.bounds:
+            return f"const {t} {instr.dest} = ({valid.render()}) ? ({t}){ref} : ({t})0;"
+        return f"const {t} {instr.dest} = ({t}){ref};"
+    if op is Opcode.ARITH:
+        return f"const {t} {instr.dest} = {arith(instr.arg, instr.srcs, instr.value_type)};"
+    if op is Opcode.CAST:
+        dt = instr.value_type
+        src = instr.srcs[0]
+        if dt is bfloat16:
+            return f"const float {instr.dest} = b2f(f2b((float){src}));"
+        if dt is float16:
+            return f"const float {instr.dest} = h2f(f2h((float){src}));"
+        return f"const {t} {instr.dest} = ({t})({src});"
+    if op is Opcode.GATHER:
+        buf, index = instr.arg
+        ref = load_expr(bufs.dtypes[buf], f"{buf}[{render_index(index, True)}]")
+        return f"const {t} {instr.dest} = ({t}){ref};"
+    raise NotImplementedError(f"{op} does not define a value")
+
+
+@dataclass
+class NestShape:
+    """A nest read as cells x reduce-space."""
+
+    outer: list[tuple[str, int]]
+    inner: list[tuple[str, int]]
+    body: list[Instr]
+    write: Instr | None  # STORE/SCATTER for elementwise; the final STORE for a register reduce
+    fold: Op | None  # ADD / MAX for reduces
+    identity: float | int | None
+    out_index: Index | None
+    accum_form: bool = False
+    reduce_dtype: DType | None = None
+    item: str = ""
+
+
+def read_nest(nest: LoopNest) -> NestShape:
+    ins = list(nest.instrs)
+    loops: dict[str, int] = {}
+    for instr in ins:
+        if instr.opcode is Opcode.LOOP:
+            loops[instr.dest] = instr.arg
+    if any(i.opcode is Opcode.ACCUM for i in ins):
+        # STORE identity over the outer loops, then LOOP(all) ... ACCUM
+        first_end = next(k for k, i in enumerate(ins) if i.opcode is Opcode.STORE)
+        init = [i for i in ins[:first_end] if i.opcode is Opcode.CONST]
+        identity = init[0].arg[0]
+        outer_vars = [i.dest for i in ins[:first_end] if i.opcode is Opcode.LOOP]
+        k = first_end
+        while ins[k].opcode is not Opcode.LOOP:
+            k += 1
+        order_vars = []
+        while ins[k].opcode is Opcode.LOOP:
+            order_vars.append(ins[k].dest)
+            k += 1
+        accum = next(i for i in ins if i.opcode is Opcode.ACCUM)
+        body = [i for i in ins[k:] if i.opcode not in (Opcode.ACCUM, Opcode.ENDLOOP, Opcode.LOOP)]
+        inner = [(v, loops[v]) for v in order_vars if v not in outer_vars]
+        return NestShape(
+            outer=[(v, loops[v]) for v in outer_vars],
+            inner=inner,
+            body=body,
+            write=None,
+            fold=accum.arg[2],
+            identity=identity,
+            out_index=accum.arg[1],
+            accum_form=True,
+            reduce_dtype=accum.dtype,
+            item=accum.srcs[0],
+        )
+    acc = next((i for i in ins if i.opcode is Opcode.ACC), None)
+    if acc is not None:
+        k_acc = ins.index(acc)
+        outer_vars = [i.dest for i in ins[:k_acc] if i.opcode is Opcode.LOOP]
+        update = next(i for i in ins if i.opcode is Opcode.UPDATE)
+        k_upd = ins.index(update)
+        inner_vars = [i.dest for i in ins[k_acc:k_upd] if i.opcode is Opcode.LOOP]
+        body = [i for i in ins[k_acc:k_upd] if i.opcode not in (Opcode.LOOP, Opcode.ENDLOOP, Opcode.ACC)]
+        store = next(i for i in ins[k_upd:] if i.opcode is Opcode.STORE)
+        return NestShape(
+            outer=[(v, loops[v]) for v in outer_vars],
+            inner=[(v, loops[v]) for v in inner_vars],
+            body=body,
+            write=store,
+            fold=update.arg,
+            identity=acc.arg,
+            out_index=store.arg[1],
+            reduce_dtype=acc.dtype,
+            item=update.srcs[0],
+        )
+    outer_vars = [i.dest for i in ins if i.opcode is Opcode.LOOP]
+    body = [i for i in ins if i.opcode not in (Opcode.LOOP, Opcode.ENDLOOP, Opcode.STORE, Opcode.SCATTER)]
+    write = next(i for i in ins if i.opcode in (Opcode.STORE, Opcode.SCATTER))
+    return NestShape(outer=[(v, loops[v]) for v in outer_vars], inner=[], body=body, write=write, fold=None, identity=None, out_index=None)
+
+
+def decode(vars_: list[tuple[str, int]], flat: str, indent: str, wide: bool) -> list[str]:
+    """Loop variables from a flat index, the last one fastest."""
+    if not vars_:
+        return []
+    scratch = "i64" if wide else "int"
+    lines = [f"{indent}{scratch} t_ = {flat};"]
+    for var, extent in reversed(vars_[1:]):
+        lines.append(f"{indent}const int {var} = (int)(t_ % {extent}); t_ /= {extent};")
+    lines.append(f"{indent}const int {vars_[0][0]} = (int)t_;")
+    return lines
+
+
+@dataclass
+class Launch:
+    name: str
+    grid: int
+    block: int
+    args: str  # "io" (inputs then out), "io_scratch" (inputs then scratch), "scratch_out"
+
+
+@dataclass
+class Planned:
+    """What one nest became: kernels to launch in order, and the scratch bytes they share."""
+
+    source: str
+    launches: list[Launch]
+    scratch_bytes: int = 0
+    notes: dict = field(default_factory=dict)
+
+
+def _vec_width(nest_shape: NestShape, bufs: Buffers, var: str, extent: int) -> int:
+    """How many consecutive values of `var` one thread takes: 16 bytes of the narrowest buffer
+    stepping along it, when the extent divides."""
+    widths = [bufs.dtypes[b].itemsize for b in bufs.dtypes]
+    v = 16 // max(1, min(widths)) if widths else 4
+    v = max(1, min(v, 8))
+    while v > 1 and extent % v:
+        v //= 2
+    return v
+
+
+def signature(name: str, nest: LoopNest, out_dtype: DType, extra: str = "") -> str:
+    params = [f"const {STORE_T[n.dtype]}* __restrict__ in{k}" for k, n in enumerate(nest.kernel.inputs)]
+    params.append(f"{STORE_T[out_dtype]}* __restrict__ out")
+    if extra:
+        params.append(extra)
+    return f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}({", ".join(params)})'
+
+
+def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
+    cells = math.prod(e for _, e in shape.outer)
+    write = shape.write
+    assert write is not None
+    out_dtype = nest.kernel.target.dtype
+    inner_var, inner_extent = shape.outer[-1] if shape.outer else ("", 1)
+    vec = _vec_width(shape, bufs, inner_var, inner_extent) if shape.outer and write.opcode is Opcode.STORE else 1
+    wide = bufs.wide_index or cells > (1 << 30)
+    lines = [signature(nest.name, nest, out_dtype) + " {"]
+    groups = cells // vec
+    lines.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {groups}LL; g += (i64)gridDim.x * {THREADS}) {{")
+    if shape.outer:
+        base_vars = shape.outer[:-1] + [(inner_var + "_b", inner_extent // vec)]
+        lines += decode(base_vars, "g", "    ", wide)
+        lines.append("#pragma unroll")
+        lines.append(f"    for (int j_ = 0; j_ < {vec}; j_++) {{")
+        lines.append(f"      const int {inner_var} = {inner_var}_b * {vec} + j_;")
+    else:
+        lines.append("    {")
+    for instr in shape.body:
+        lines.append("      " + value_line(instr, bufs))
+    buf, index = write.arg
+    if write.opcode is Opcode.SCATTER:
+        if out_dtype not in (float32, float64, int32):
+            raise NotImplementedError(f"the hip device cannot scatter {out_dtype}; cast the table to float32 or int32")
+        lines.append(f"      atomicAdd(&{buf}[{render_index(index, True)}], ({STORE_T[out_dtype]}){write.srcs[0]});")
+    else:
+        lines.append(f"      {buf}[{render_index(index, wide)}] = {store_expr(out_dtype, write.srcs[0])};")
+    lines += ["    }", "  }", "}"]
+    grid = max(1, min(-(-groups // THREADS), 1 << 20))
+    return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")])
+
+
+def _fold(op: Op, acc: str, x: str) -> str:
+    return f"{acc} = fadd({acc}, {x});" if op is Op.ADD else f"{acc} = fmax_nan({acc}, {x});"
+
+
+def stride_one_var(nest: LoopNest, shape: NestShape) -> str | None:
+    """The loop variable along which the most loaded bytes are contiguous (coefficient 1)."""
+    sizes = {f"in{k}": math.prod(n.shape) * n.dtype.itemsize for k, n in enumerate(nest.kernel.inputs)}
+    weight: dict[str, int] = {}
+    for instr in shape.body:
+        if instr.opcode is Opcode.LOAD:
+            buf, index, _ = instr.arg
+            for var, coeff in index.terms:
+                if coeff == 1:
+                    weight[var] = weight.get(var, 0) + sizes.get(buf, 0)
+    if not weight:
+        return None
+    return max(weight, key=lambda v: weight[v])
+
+
+def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
+    cells = math.prod(e for _, e in shape.outer)
+    R = math.prod(e for _, e in shape.inner)
+    rdt = shape.reduce_dtype
+    assert rdt is not None and shape.fold is not None
+    acc_dt = accumulate_in(rdt)
+    acc_t = VALUE_T[acc_dt]
+    out_dtype = nest.kernel.target.dtype
+    wide = bufs.wide_index or cells * R > (1 << 30)
+    ident = literal(shape.identity, acc_dt)
+    item = shape.item
+    out_ref = f"out[{render_index(shape.out_index, wide)}]"
+    fold = shape.fold
+    wave_fold = "wave_fold_add" if fold is Op.ADD else "wave_fold_max"
+
+    # how many threads own a cell: lanes go along whichever loop variable the most bytes are
+    # stride-1 in. The IR's own nesting (its ACCUM form) was chosen for a CPU's inner loop and
+    # can put a row index innermost merely because small per-row vectors are stride-1 along it.
+    along = stride_one_var(nest, shape)
+    columns = along is not None and along not in {v for v, _ in shape.inner}
+    if columns and cells >= 1024:
+        group = 1
+        shape.outer = [o for o in shape.outer if o[0] != along] + [o for o in shape.outer if o[0] == along]
+    elif R < 64 or (cells >= (1 << 20) and R <= 256):
+        group = 1
+    elif R < 4096:
+        group = 64
+    else:
+        group = THREADS
+    parts = 1
+    if group == THREADS and cells < 1024 and R >= (1 << 15):
+        parts = max(1, min(1024 // max(cells, 1), -(-R // (1 << 13))))
+
+    body = ["      " + value_line(i, bufs) for i in shape.body]
+    inner_var, inner_extent = shape.inner[-1]
+
+    if group == 1:
+        lines = [signature(nest.name, nest, out_dtype) + " {"]
+        lines.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {cells}LL; g += (i64)gridDim.x * {THREADS}) {{")
+        lines += decode(shape.outer, "g", "    ", wide)
+        lines.append(f"    {acc_t} acc = {ident};")
+        for var, extent in shape.inner:
+            lines.append(f"    for (int {var} = 0; {var} < {extent}; {var}++) {{")
+        lines += body
+        lines.append("      " + _fold(fold, "acc", f"({acc_t}){item}"))
+        lines += ["    }"] * len(shape.inner)
+        lines.append(f"    {out_ref} = {store_expr(out_dtype, 'acc')};")
+        lines += ["  }", "}"]
+        grid = max(1, min(-(-cells // THREADS), 1 << 20))
+        return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes={"group": 1})
+
+    vec = _vec_width(shape, bufs, inner_var, inner_extent)
+    chunks = R // vec  # vec divides the innermost extent, hence R
+    per_part = -(-chunks // parts)
+    base_vars = shape.inner[:-1] + [(inner_var + "_b", inner_extent // vec)]
+
+    def strided_loop(first: str, stop: str, step: int) -> list[str]:
+        out = [f"    for (i64 c_ = {first}; c_ < {stop}; c_ += {step}) {{"]
+        out += decode(base_vars, "c_", "      ", True)
+        out.append("#pragma unroll")
+        out.append(f"      for (int j_ = 0; j_ < {vec}; j_++) {{")
+        out.append(f"      const int {inner_var} = {inner_var}_b * {vec} + j_;")
+        out += body
+        out.append("      " + _fold(fold, "acc", f"({acc_t}){item}"))
+        out += ["      }", "    }"]
+        return out
+
+    waves = THREADS // 64
+    if group == 64:
+        lines = [signature(nest.name, nest, out_dtype) + " {"]
+        lines.append("  const int lane = threadIdx.x & 63;")
+        lines.append(f"  for (i64 g = blockIdx.x * (i64){waves} + (threadIdx.x >> 6); g < {cells}LL; g += (i64)gridDim.x * {waves}) {{")
+        lines += decode(shape.outer, "g", "    ", wide)
+        lines.append(f"    {acc_t} acc = {ident};")
+        lines += strided_loop("lane", f"{chunks}LL", 64)
+        lines.append(f"    acc = {wave_fold}(acc);")
+        lines.append(f"    if (lane == 0) {out_ref} = {store_expr(out_dtype, 'acc')};")
+        lines += ["  }", "}"]
+        grid = max(1, min(-(-cells // waves), 1 << 20))
+        return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes={"group": 64, "vec": vec})
+
+    # a workgroup per (cell, part)
+    def block_fold(lines: list[str]) -> None:
+        lines.append(f"    acc = {wave_fold}(acc);")
+        lines.append(f"    __shared__ {acc_t} lds_[{waves}];")
+        lines.append("    if ((threadIdx.x & 63) == 0) lds_[threadIdx.x >> 6] = acc;")
+        lines.append("    __syncthreads();")
+        lines.append("    if (threadIdx.x == 0) {")
+        lines.append("      acc = lds_[0];")
+        for w in range(1, waves):
+            lines.append("      " + _fold(fold, "acc", f"lds_[{w}]"))
+
+    if parts == 1:
+        lines = [signature(nest.name, nest, out_dtype) + " {"]
+        lines.append(f"  for (i64 g = blockIdx.x; g < {cells}LL; g += gridDim.x) {{")
+        lines += decode(shape.outer, "g", "    ", wide)
+        lines.append(f"    {acc_t} acc = {ident};")
+        lines += strided_loop("threadIdx.x", f"{chunks}LL", THREADS)
+        block_fold(lines)
+        lines.append(f"      {out_ref} = {store_expr(out_dtype, 'acc')};")
+        lines += ["    }", "    __syncthreads();", "  }", "}"]
+        grid = max(1, min(cells, 1 << 20))
+        return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes={"group": THREADS, "vec": vec})
+
+    # split: partials then an ordered fold per cell
+    part_name = nest.name + "_part"
+    params = [f"const {STORE_T[n.dtype]}* __restrict__ in{k}" for k, n in enumerate(nest.kernel.inputs)]
+    params.append(f"{acc_t}* __restrict__ scratch")
+    lines = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {part_name}({", ".join(params)}) {{']
+    lines.append(f"  const i64 g = blockIdx.x / {parts}, p_ = blockIdx.x % {parts};")
+    lines += decode(shape.outer, "g", "  ", wide)
+    lines.append(f"  {acc_t} acc = {ident};")
+    lines.append(f"  const i64 stop_ = (p_ + 1) * {per_part}LL < {chunks}LL ? (p_ + 1) * {per_part}LL : {chunks}LL;")
+    lines += strided_loop(f"p_ * {per_part}LL + threadIdx.x", "stop_", THREADS)
+    block_fold(lines)
+    lines.append("      scratch[blockIdx.x] = acc;")
+    lines += ["    }", "}"]
+    final = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {nest.name}(const {acc_t}* __restrict__ scratch, {STORE_T[out_dtype]}* __restrict__ out) {{']
+    final.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {cells}LL; g += (i64)gridDim.x * {THREADS}) {{")
+    final += decode(shape.outer, "g", "    ", wide)
+    final.append(f"    {acc_t} acc = scratch[g * {parts}];")
+    final.append(f"    for (int p_ = 1; p_ < {parts}; p_++) " + _fold(fold, "acc", f"scratch[g * {parts} + p_]"))
+    final.append(f"    {out_ref} = {store_expr(out_dtype, 'acc')};")
+    final += ["  }", "}"]
+    source = "\n".join(lines) + "\n" + "\n".join(final)
+    launches = [
+        Launch(part_name, cells * parts, THREADS, "io_scratch"),
+        Launch(nest.name, max(1, min(-(-cells // THREADS), 1 << 20)), THREADS, "scratch_out"),
+    ]
+    return Planned(source, launches, scratch_bytes=cells * parts * acc_dt.itemsize, notes={"parts": parts, "vec": vec})
+
+
+def plan_nest(nest: LoopNest) -> Planned:
+    kernel = nest.kernel
+    dtypes = {f"in{k}": n.dtype for k, n in enumerate(kernel.inputs)}
+    dtypes["out"] = kernel.target.dtype
+    biggest = max([math.prod(n.shape) for n in kernel.inputs] + [math.prod(kernel.target.shape)])
+    bufs = Buffers(dtypes, wide_index=biggest >= (1 << 31) - 1)
+    shape = read_nest(nest)
+    if shape.fold is None:
+        return plan_elementwise(nest, shape, bufs)
+    return plan_reduce(nest, shape, bufs)
+
+
+def _launcher(dev, fn: int, launch: Launch, nin: int):
+    api = dev.api
+    nargs = nin + 1
+    slots = (ctypes.c_void_p * nargs)()
+    params = (ctypes.c_void_p * nargs)(*[ctypes.addressof(slots) + k * ctypes.sizeof(ctypes.c_void_p) for k in range(nargs)])
+    grid, block = launch.grid, launch.block
+
+    def run(ptrs: list[int]) -> None:
+        for k, p in enumerate(ptrs):
+            slots[k] = p
+        runtime.check(api.hipModuleLaunchKernel(fn, grid, 1, 1, block, 1, 1, 0, None, params, None), f"launching {launch.name}")
+
+    return run
+
+
+def nest_runners(dev, nests: list[LoopNest]):
+    """Compile every nest of a plan into one hipRTC program; one runner per nest, in order."""
+    plans = [plan_nest(n) for n in nests]
+    source = PRELUDE + "\n".join(p.source for p in plans)
+    names = [launch.name for p in plans for launch in p.launches]
+    functions = runtime.load_functions(source, names)
+    runners = []
+    for nest, plan in zip(nests, plans):
+        nin = len(nest.kernel.inputs)
+        launchers = []
+        for launch in plan.launches:
+            count = nin + 1 if launch.args in ("io", "io_scratch") else 2
+            launchers.append((launch.args, _launcher(dev, functions[launch.name], launch, count - 1)))
+        runners.append(_make_runner(dev, launchers, plan.scratch_bytes))
+    return runners
+
+
+def _make_runner(dev, launchers, scratch_bytes: int):
+    held: list = []
+
+    def run(inputs: list, outs: list) -> None:
+        if scratch_bytes and not held:
+            held.append(dev._alloc(scratch_bytes))
+        ins = [b.ptr for b in inputs]
+        for kind, launch in launchers:
+            if kind == "io":
+                launch(ins + [outs[0].ptr])
+            elif kind == "io_scratch":
+                launch(ins + [held[0].ptr])
+            else:
+                launch([held[0].ptr, outs[0].ptr])
+
+    return run

@@ -1,0 +1,50 @@
+"""The graph corpus every device is run through (the reference's tests/conftest.py:76-93 set),
+and the check that diffs a device against the numpy oracle on the same graph."""
+
+from __future__ import annotations
+
+import numpy as np
+
+from limn_amd import device as limn_device
+from limn_amd.dtypes import from_storage
+from limn_amd.ops import HALF_FLOATS
+from oracle.numpy_device import NumpyDevice
+
+limn_device.register("numpy", NumpyDevice)
+
+GRAPHS = {
+    "elementwise": lambda a, b: (a + b) * 2.0 - a,
+    "relu": lambda a, b: (a * b).relu() + 1.0,
+    "unary math": lambda a, b: (a * a + 1.0).log().exp().sqrt(),
+    "divide": lambda a, b: a / (b * b + 0.5),
+    "where": lambda a, b: (a < b).where(a, b),
+    "cast round trip": lambda a, b: (a * 4.0).int().float() + 0.5,
+    "sum an axis": lambda a, b: (a + b).sum(axis=1),
+    "sum everything": lambda a, b: (a * b).sum(),
+    "max keepdim": lambda a, b: (a * b).max(axis=0, keepdim=True),
+    "mean": lambda a, b: (a + b).mean(axis=1),
+    "matmul": lambda a, b: a @ b.transpose(),
+    "softmax": lambda a, b: (a + b).softmax(axis=1),
+    "log softmax": lambda a, b: (a * b).log_softmax(axis=0),
+    "padded reduce": lambda a, b: a.pad(((1, 1), (0, 2))).sum(axis=1),
+    "movement then reduce": lambda a, b: (a.transpose() * 2.0).sum(axis=0),
+    "reduce then elementwise": lambda a, b: (a.sum(axis=1, keepdim=True) * b).relu(),
+}
+
+
+def check(dev, t, rtol: float = 1e-5, atol: float = 1e-5, exact: bool = False) -> None:
+    """Realize `t` on `dev` first, then on the numpy oracle (which retires the node), and diff
+    (reference tests/conftest.py:52-69). Half widths compare widened to float32."""
+    got = from_storage(dev.copyout(dev.execute([t.node])[0]), t.dtype, t.shape)
+    saved = limn_device.active_device
+    limn_device.active_device = NumpyDevice()
+    try:
+        want = t.numpy()
+    finally:
+        limn_device.active_device = saved
+    if exact:
+        np.testing.assert_array_equal(got, want)
+        return
+    if t.dtype in HALF_FLOATS:
+        got, want = got.astype(np.float32), want.astype(np.float32)
+    np.testing.assert_allclose(got, want, rtol=rtol, atol=atol)

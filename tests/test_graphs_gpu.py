@@ -1,0 +1,265 @@
+"""The hip device's compiled-device contract on the MI355X (reference
+tests/test_compiled_devices.py, test_backend_cuda.py, test_dtypes.py and test_attention.py's GPU
+cases): the graph corpus, every reduce form, gathers and scatters, dtypes, the assign
+transaction, plan reuse, and attention through the Tensor API, each diffed against the numpy
+oracle on the same graph. Tensors are created under the numpy device (host buffers) and the hip
+device uploads them per batch, as the reference's GPU tests do."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from graphs import GRAPHS, check
+from limn_amd import device as limn_device
+from limn_amd.ops import Op, bfloat16, float16, float32, float64, int8, int16, int32, topological
+from limn_amd.tensor import Tensor, grad
+
+pytestmark = pytest.mark.gpu
+
+rng = np.random.default_rng(7)
+
+
+def randf(*shape: int) -> np.ndarray:
+    return rng.uniform(-2, 2, shape).astype(np.float32)
+
+
+@pytest.fixture(autouse=True)
+def on_numpy():
+    limn_device.set_device("numpy")
+    yield
+
+
+@pytest.mark.parametrize("name", list(GRAPHS))
+def test_corpus(hipdev, name):
+    a, b = Tensor(randf(5, 7)), Tensor(randf(5, 7))
+    check(hipdev, GRAPHS[name](a, b))
+
+
+@pytest.mark.parametrize("name", ["softmax", "sum an axis", "log softmax", "movement then reduce", "matmul"])
+def test_corpus_at_size(hipdev, name):
+    a, b = Tensor(randf(300, 300)), Tensor(randf(300, 300))
+    check(hipdev, GRAPHS[name](a, b), rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize(
+    "shape,axis",
+    [((3, 10), 1), ((9000, 70), 1), ((700, 3000), 1), ((64, 9000), 1), ((4, 300000), 1), ((3000, 40), 0), ((40, 3000), 0), ((2, 3, 4000, 5), (1, 2))],
+    ids=["tiny", "thread-per-cell", "wave-per-cell", "workgroup-per-cell", "split", "accum-columns", "accum-few-columns", "two-axes"],
+)
+def test_every_reduce_form(hipdev, shape, axis):
+    x = Tensor(rng.standard_normal(shape).astype(np.float32))
+    check(hipdev, x.sum(axis=axis), rtol=1e-4, atol=1e-3)
+    check(hipdev, x.max(axis=axis), exact=True)
+
+
+def test_max_propagates_nan(hipdev):
+    data = rng.standard_normal((4, 5000)).astype(np.float32)
+    data[1, 4321] = np.nan
+    data[3, 0] = np.nan
+    got = Tensor(data).max(axis=1)
+    check(hipdev, got, exact=True)
+
+
+def test_reduce_to_a_scalar(hipdev):
+    x = Tensor(rng.standard_normal((1000, 1000)).astype(np.float32))
+    check(hipdev, x.sum(), rtol=1e-4, atol=1e-2)
+    check(hipdev, (x * x).mean(), rtol=1e-4, atol=1e-4)
+
+
+def test_grid_stride_covers_everything(hipdev):
+    n = 2 * 4096 * 256 + 3
+    x = Tensor(np.arange(n, dtype=np.float32))
+    check(hipdev, x * 2.0 + 1.0, exact=True)
+
+
+def test_gather_rows(hipdev):
+    table = Tensor(randf(50, 16))
+    idx = Tensor(rng.integers(0, 50, size=(7, 9)).astype(np.int32))
+    check(hipdev, table[idx], exact=True)
+
+
+def test_scatter_with_repeats(hipdev):
+    """512 values land on one row: atomics collide, the total still matches (reference
+    tests/test_backend_cuda.py:125-131)."""
+    values = Tensor(randf(512, 8))
+    idx = Tensor(np.zeros(512, dtype=np.int32))
+    from limn_amd.tensor import scatter_rows
+
+    check(hipdev, scatter_rows(values, idx, (4, 8)), rtol=1e-4, atol=1e-4)
+
+
+def test_scatter_int32_is_exact(hipdev):
+    from limn_amd.tensor import scatter_rows
+
+    values = Tensor(rng.integers(-1000, 1000, size=(300, 5)).astype(np.int32))
+    idx = Tensor(rng.integers(0, 6, size=300).astype(np.int32))
+    check(hipdev, scatter_rows(values, idx, (6, 5)), exact=True)
+
+
+def test_scatter_refuses_half_widths(hipdev):
+    from limn_amd.tensor import scatter_rows
+
+    values = Tensor(randf(8, 4), dtype=bfloat16)
+    idx = Tensor(np.zeros(8, dtype=np.int32))
+    with pytest.raises(NotImplementedError):
+        hipdev.execute([scatter_rows(values, idx, (2, 4)).node])
+
+
+def test_gather_backward_scatters(hipdev):
+    table = Tensor(randf(10, 4), requires_grad=True)
+    idx = Tensor(rng.integers(0, 10, size=(6, 3)).astype(np.int32))
+    (g,) = grad((table[idx] * Tensor(randf(6, 3, 4))).sum(), [table])
+    check(hipdev, g, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype,tol", [(float64, 1e-12), (float16, 2e-3), (bfloat16, 1e-2)], ids=str)
+def test_float_dtypes(hipdev, dtype, tol):
+    """Half widths: the oracle rounds every node to its dtype while a kernel keeps fused
+    intermediates in float, so sums over K products get an atol that grows with K."""
+    a, b = Tensor(randf(9, 17), dtype=dtype), Tensor(randf(9, 17), dtype=dtype)
+    for name in ("elementwise", "softmax", "max keepdim"):
+        check(hipdev, GRAPHS[name](a, b), rtol=tol, atol=tol * 2)
+    for name in ("sum an axis", "matmul"):
+        check(hipdev, GRAPHS[name](a, b), rtol=tol, atol=tol * 16)
+
+
+def test_half_sums_total_in_float32(hipdev):
+    """1024 halves of 1 + tiny: a float16 running total would stall (reference
+    tests/test_dtypes.py:207-216); the kernel totals in float32 and rounds once."""
+    x = Tensor(np.full((2, 4096), 1.0, dtype=np.float32), dtype=float16)
+    check(hipdev, x.sum(axis=1), exact=True)
+
+
+@pytest.mark.parametrize("dtype", [int32, int16, int8], ids=str)
+def test_int_dtypes_wrap_exactly(hipdev, dtype):
+    a = Tensor(rng.integers(-100, 100, size=(20, 30)), dtype=dtype)
+    b = Tensor(rng.integers(-100, 100, size=(20, 30)), dtype=dtype)
+    check(hipdev, (a * b + a).sum(axis=1), exact=True)
+    check(hipdev, (a < b).where(a, b * b), exact=True)
+
+
+def test_int8_sum_of_300_ones_wraps_to_44(hipdev):
+    x = Tensor(np.ones(300, dtype=np.int8), dtype=int8)
+    got = x.sum()
+    check(hipdev, got, exact=True)
+    limn_device.set_device("numpy")
+    assert got.item() == 44
+
+
+def test_bf16_nan_store(hipdev):
+    x = Tensor(np.array([1.0, np.nan, -2.0], dtype=np.float32), dtype=bfloat16)
+    got = hipdev.execute([(x * 1.0).node])[0]
+    vals = hipdev.copyout(got).view(np.uint16)
+    assert np.isnan((vals.astype(np.uint32) << 16).view(np.float32)[1])
+
+
+def test_assign_is_deferred_until_every_sink_is_computed(hipdev):
+    """Both sinks read `w` before the assign commits (reference tests/test_compiled_devices.py:73-98)."""
+    limn_device.active_device = hipdev
+    w = Tensor(np.ones(4, dtype=np.float32))
+    read = w * 2.0
+    w.assign(w + 1.0)
+    bufs = hipdev.execute([read.node, w.node])
+    got_read = hipdev.copyout(bufs[0]).view(np.float32)
+    np.testing.assert_array_equal(got_read, np.full(4, 2.0, np.float32))
+    np.testing.assert_array_equal(hipdev.copyout(bufs[1]).view(np.float32), np.full(4, 2.0, np.float32))
+
+
+def test_one_plan_for_a_repeated_graph(hipdev):
+    before = len(hipdev.plans)
+    for _ in range(3):
+        a, b = Tensor(randf(6, 6)), Tensor(randf(6, 6))
+        hipdev.execute([((a + b) * 3.0).node])
+    assert len(hipdev.plans) == before + 1
+
+
+def test_a_changed_const_is_a_new_plan(hipdev):
+    a = Tensor(randf(6, 6))
+    before = len(hipdev.plans)
+    hipdev.execute([(a * 3.0).node])
+    hipdev.execute([(a * 4.0).node])
+    assert len(hipdev.plans) == before + 2
+
+
+# ---- attention through the Tensor API (the CUSTOM seam) ----
+
+
+def _attention_grads(q_shape, k_shape, v_shape, causal, dtype=float32, live=None):
+    data = [rng.standard_normal(s).astype(np.float32) for s in (q_shape, k_shape, v_shape)]
+    out_shape = np.broadcast_shapes(q_shape[:-2], k_shape[:-2], v_shape[:-2]) + (q_shape[-2], v_shape[-1])
+    w = rng.standard_normal(out_shape).astype(np.float32)
+    q, k, v = (Tensor(d, dtype=dtype, requires_grad=True) for d in data)
+    mask = None
+    if live is not None:
+        mask = Tensor(np.broadcast_to(np.arange(k_shape[-2]) < live, k_shape[:-1]).astype(np.float32))
+    out = q.attention(k, v, causal=causal, key_mask=mask)
+    return out, grad((out * Tensor(w, dtype=dtype)).sum(), [q, k, v])
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("dtype,tol", [(float32, 1e-4), (float16, 4e-3), (bfloat16, 3e-2)], ids=str)
+def test_attention_backward_through_the_tensor_api(hipdev, causal, dtype, tol):
+    out, grads = _attention_grads((2, 3, 64, 16), (2, 3, 64, 16), (2, 3, 64, 24), causal, dtype)
+    check(hipdev, out, rtol=tol, atol=tol)
+    for g in grads:
+        check(hipdev, g, rtol=tol, atol=tol)
+
+
+def test_attention_backward_graph_is_custom(hipdev):
+    out, grads = _attention_grads((2, 48, 8), (2, 48, 8), (2, 48, 12), True)
+    nodes = topological([g.node for g in grads])
+    names = {n.arg.name for n in nodes if n.op is Op.CUSTOM}
+    assert names == {"sdpa", "sdpa_bwd_q", "sdpa_bwd_kv"}
+    assert not [n for n in nodes if n.shape[-2:] == (48, 48)]
+
+
+@pytest.mark.parametrize("shapes", [((1, 3, 16, 8), (4, 3, 16, 8), (4, 1, 16, 12)), ((40, 8), (72, 8), (72, 12))], ids=["broadcast", "rectangular"])
+def test_attention_broadcast_and_rectangular(hipdev, shapes):
+    out, grads = _attention_grads(*shapes, causal=False)
+    check(hipdev, out)
+    for g in grads:
+        check(hipdev, g, rtol=1e-4, atol=1e-4)
+
+
+def test_attention_key_mask_through_the_api(hipdev):
+    out, grads = _attention_grads((2, 100, 16), (2, 100, 16), (2, 100, 16), True, live=66)
+    check(hipdev, out)
+    for g in grads:
+        check(hipdev, g, rtol=1e-4, atol=1e-4)
+
+
+def test_two_attentions_on_one_input(hipdev):
+    q, k, v = (Tensor(randf(2, 3, 32, 8)) for _ in range(3))
+    check(hipdev, q.attention(k, v, causal=True) + q.attention(k, v, causal=True))
+
+
+def test_mfma_attention_through_the_api(hipdev):
+    out, grads = _attention_grads((2, 4, 256, 64), (2, 4, 256, 64), (2, 4, 256, 64), True, bfloat16)
+    check(hipdev, out, rtol=1e-2, atol=1e-2)
+    for g in grads:
+        check(hipdev, g, rtol=3e-2, atol=3e-2)
+
+
+def test_config2_full_size(hipdev):
+    """BASELINE config 2 at full size: x f32 (8192, 8192) from default_rng(2), row softmax then
+    LayerNorm (gamma 1, beta 0, eps 1e-5). Rows are independent, so 16 sampled rows are diffed
+    against the oracle run on just those rows; every row must be finite with mean ~ 0."""
+    N = 8192
+    x_host = np.random.default_rng(2).standard_normal((N, N), dtype=np.float32)
+
+    def chain(x):
+        w, b = Tensor.ones((N,)), Tensor.zeros((N,))
+        y = x.softmax(-1)
+        c = y - y.mean(axis=-1, keepdim=True)
+        var = (c * c).mean(axis=-1, keepdim=True)
+        return c / (var + 1e-5).sqrt() * w + b
+
+    limn_device.active_device = hipdev
+    out = chain(Tensor(x_host)).numpy()
+    assert np.isfinite(out).all()
+    np.testing.assert_allclose(out.mean(axis=1), 0.0, atol=1e-6)
+    rows = np.random.default_rng(0).choice(N, size=16, replace=False)
+    limn_device.set_device("numpy")
+    want = chain(Tensor(x_host[rows])).numpy()
+    np.testing.assert_allclose(out[rows], want, rtol=1e-5, atol=1e-5)
