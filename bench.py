@@ -43,7 +43,7 @@ def parse() -> argparse.Namespace:
     p.add_argument(
         "--workload",
         default="c4",
-        choices=["c4", "copy", "c2"],
+        choices=["c4", "copy", "c2", "c3"],
         help="c4: the headline attention step; copy: a plain 256 MiB device copy kernel, the "
         "known-size reference that scales rocprofv3's FETCH_SIZE/WRITE_SIZE counters",
     )
@@ -230,6 +230,57 @@ def bench_c2(dev, steps: int, warmup: int) -> dict:
     }
 
 
+def bench_c3(dev, steps: int, warmup: int) -> dict:
+    """bf16 A(4096x4096) @ B(4096x4096) with f32 accumulate, relu and a bf16
+    store; A, B ~ N(0, 0.125^2) from default_rng(3). The scheduler gives two nests (the SUM
+    contraction, which the device lowers to its MFMA kernel, and the relu); both are timed."""
+    from limn_amd import device as limn_device
+    from limn_amd.dtypes import bf16_bits
+    from limn_amd.ops import bfloat16
+    from limn_amd.tensor import Tensor
+
+    n = 4096
+    r = np.random.default_rng(3)
+    limn_device.active_device = dev
+    a = Tensor(bf16_bits(r.standard_normal((n, n), dtype=np.float32) * 0.125), dtype=bfloat16)
+    b = Tensor(bf16_bits(r.standard_normal((n, n), dtype=np.float32) * 0.125), dtype=bfloat16)
+    out = (a @ b).relu()
+    plan, sources = record_plan(dev, [out.node])
+    ncalls = len(plan.calls)
+    for _ in range(warmup):
+        timed_calls(dev, plan, sources, Events(dev.api, ncalls + 1), 0)
+    dev.finish()
+    ev = Events(dev.api, steps * (ncalls + 1))
+    for s_ in range(steps):
+        timed_calls(dev, plan, sources, ev, s_ * (ncalls + 1))
+    dev.finish()
+    per = np.zeros(ncalls)
+    for s_ in range(steps):
+        base = s_ * (ncalls + 1)
+        per += [ev.ms(base + i, base + i + 1) for i in range(ncalls)]
+    per /= steps
+    flops = 2.0 * n**3
+    mm = float(per[0])
+    return {
+        "metric": "matmul TFLOP/s",
+        "value": round(flops / (float(per.sum()) * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(float(per.sum()), 4),
+        "dtype": "bf16",
+        "config": {"workload": "C3 bf16 4096^3 contraction + relu + bf16 store", "flop_per_step": flops},
+        "kernels_ms": [round(float(t), 4) for t in per],
+        "roofline": {
+            "kernel": "matmul_mfma (the contraction nest)",
+            "bound": "mfma",
+            "achieved": round(flops / (mm * 1e-3) / 1e12, 2),
+            "peak": MFMA_BF16_PEAK / 1e12,
+            "unit": "TFLOP/s",
+            "frac": round(flops / (mm * 1e-3) / MFMA_BF16_PEAK, 4),
+            "traffic": None,
+        },
+    }
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -242,6 +293,11 @@ def main() -> int:
         from limn_amd.hip.device import HipDevice
 
         print(json.dumps(bench_c2(HipDevice(), args.steps, args.warmup)), flush=True)
+        return 0
+    if args.workload == "c3":
+        from limn_amd.hip.device import HipDevice
+
+        print(json.dumps(bench_c3(HipDevice(), args.steps, args.warmup)), flush=True)
         return 0
     from limn_amd.dtypes import bf16_bits, bf16_values
     from limn_amd.hip.device import HipDevice
@@ -355,7 +411,7 @@ def main() -> int:
         inputs = [bf16_values(h.reshape(B, H, S, D)[:1, :1]) for h in host]
         line["cpu_baseline"] = cpu_baseline(*inputs, scale, B, H, step_flops)
     del q, k, v, do, out, lse, dq, dk, dv, delta, lse_node, o_node, l_node, dq_node, dk_node
-    line["workloads"] = {"C2": bench_c2(dev, args.steps, args.warmup)}
+    line["workloads"] = {"C2": bench_c2(dev, args.steps, args.warmup), "C3": bench_c3(dev, args.steps, args.warmup)}
     print(json.dumps(line), flush=True)
     return 0
 

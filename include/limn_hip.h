@@ -89,6 +89,22 @@ int limn_hip_sdpa_bwd_kv(const void* q, const void* k, const void* v, const void
                          const void* key_mask, void* dk, void* dv, int dtype, int64_t batch, int64_t t_q, int64_t t_k,
                          int64_t hd, int64_t hd_v, int causal, double scale, void* stream);
 
+/*
+ * Dense contraction on matrix cores: c[b, m, n] = epilogue(sum_k a[b, m, k] * b[b, k, n]), bf16 or
+ * f16 operands and result, f32 accumulation. Strides are in elements; each operand must be
+ * contiguous along k or along its row (m / n) with the other stride a multiple of 8.
+ * epilogue: 0 = none, 1 = relu before the store. Replaces the tiled SIMT matmul the reference
+ * emits for a dense contraction nest, limn/cuda_emit.py:376-685 (matmul_shape, emit_tiled).
+ */
+int limn_hip_matmul(const void* a, const void* b, void* c, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+                    int64_t a_batch, int64_t a_m, int64_t a_k, int64_t b_batch, int64_t b_k, int64_t b_n, int64_t c_batch,
+                    int64_t c_m, int64_t c_n, int epilogue, void* stream);
+
+/* 1 when limn_hip_matmul has a kernel for this dtype and operand layout, else 0 (the device
+ * then keeps the contraction on the general reduce kernels). */
+int limn_hip_matmul_supported(int dtype, int64_t M, int64_t N, int64_t K, int64_t a_batch, int64_t a_m, int64_t a_k,
+                              int64_t b_batch, int64_t b_k, int64_t b_n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include "matmul.h"
 #include "sdpa.h"
 
 namespace limn {
@@ -117,6 +118,30 @@ int limn_hip_sdpa_bwd_kv(const void* q, const void* k, const void* v, const void
   SdpaArgs a = {q,     k,   v,   dout, lse,  delta,       key_mask, dk,   dv, dtype,
                 batch, t_q, t_k, hd,   hd_v, causal != 0, scale,    (hipStream_t)stream};
   return run(SDPA_BWD_KV, a);
+}
+
+int limn_hip_matmul(const void* a, const void* b, void* c, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+                    int64_t a_batch, int64_t a_m, int64_t a_k, int64_t b_batch, int64_t b_k, int64_t b_n, int64_t c_batch,
+                    int64_t c_m, int64_t c_n, int epilogue, void* stream) {
+  MatmulShape s = {batch, M, N, K, a_batch, a_m, a_k, b_batch, b_k, b_n, c_batch, c_m, c_n};
+  if (dtype != LIMN_HIP_BFLOAT16 && dtype != LIMN_HIP_FLOAT16)
+    return fail(LIMN_HIP_EUNSUPPORTED, "matmul: the MFMA contraction takes bfloat16 or float16, not dtype code %d", dtype);
+  if (batch < 1 || M < 1 || N < 1 || K < 1)
+    return fail(LIMN_HIP_EINVAL, "matmul: sizes must be positive (batch %lld, M %lld, N %lld, K %lld)", (long long)batch,
+                (long long)M, (long long)N, (long long)K);
+  if (a == nullptr || b == nullptr || c == nullptr) return fail(LIMN_HIP_EINVAL, "matmul: null buffer");
+  if (epilogue != MATMUL_EPILOGUE_NONE && epilogue != MATMUL_EPILOGUE_RELU)
+    return fail(LIMN_HIP_EINVAL, "matmul: unknown epilogue %d", epilogue);
+  if (!matmul_layout_ok(s))
+    return fail(LIMN_HIP_EUNSUPPORTED, "matmul: operands must be contiguous along m/n or k with 16-byte aligned rows");
+  if (((uintptr_t)a | (uintptr_t)b) % 16 != 0) return fail(LIMN_HIP_EUNSUPPORTED, "matmul: operands must be 16-byte aligned");
+  return launch_matmul(a, b, c, dtype, s, epilogue, (hipStream_t)stream);
+}
+
+int limn_hip_matmul_supported(int dtype, int64_t M, int64_t N, int64_t K, int64_t a_batch, int64_t a_m, int64_t a_k,
+                              int64_t b_batch, int64_t b_k, int64_t b_n) {
+  MatmulShape s = {1, M, N, K, a_batch, a_m, a_k, b_batch, b_k, b_n, 0, 0, 0};
+  return (dtype == LIMN_HIP_BFLOAT16 || dtype == LIMN_HIP_FLOAT16) && M > 0 && N > 0 && K > 0 && matmul_layout_ok(s);
 }
 
 }  // extern "C"

@@ -1,0 +1,22 @@
+// Internal launch interface of the dense-contraction kernel (matmul.hip).
+#pragma once
+
+#include "common.h"
+
+namespace limn {
+
+// C[b, m, n] = sum_k A[b, m, k] * B[b, k, n]; all strides in elements.
+struct MatmulShape {
+  int64_t batch, M, N, K;
+  int64_t a_batch, a_m, a_k;
+  int64_t b_batch, b_k, b_n;
+  int64_t c_batch, c_m, c_n;
+};
+
+enum { MATMUL_EPILOGUE_NONE = 0, MATMUL_EPILOGUE_RELU = 1 };
+
+// 1 when every operand is contiguous along one of its two dims with 16-byte aligned rows.
+int matmul_layout_ok(const MatmulShape& s);
+int launch_matmul(const void* a, const void* b, void* c, int dtype, const MatmulShape& s, int epilogue, hipStream_t stream);
+
+}  // namespace limn

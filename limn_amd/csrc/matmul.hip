@@ -1,0 +1,239 @@
+// Dense contraction on CDNA4 matrix cores: C[b, m, n] = sum_k A[b, m, k] * B[b, k, n] with bf16 or
+// f16 operands, f32 accumulation, and an optional fused epilogue (relu) before the store.
+//
+// This is what a limn loop nest becomes when it is a dense contraction (a SUM over the last
+// axis of a product of two buffers that share only the reduce and batch variables): the
+// `A @ B` spelling of limn/tensor.py:486-496 lowers to exactly that nest (reference
+// limn/cuda_emit.py:376-505 detects the same shape and emits a SIMT tile).
+//
+// Tiling: a 256-thread workgroup computes a BM x BN tile (256 x 256, or 128 x 128 when the
+// larger tile would leave compute units idle); its 4 waves are 2 x 2, each owning
+// (BM/2) x (BN/2) = TM x TN accumulators of v_mfma_f32_32x32x16 (32x32 outputs, 16-deep k per
+// instruction), so per 16-deep step a wave reads TM + TN operands from LDS for TM * TN MFMAs.
+// K advances BK = 64 per stage through a double-buffered LDS: the next stage's global loads are
+// in registers while the current stage is multiplied.
+//
+// LDS holds both operands k-contiguous (A as [m][k], B as [n][k], rows padded by 8 elements
+// so 16-byte reads across a 32-row operand are conflict-free), so each MFMA operand is one
+// ds_read_b128. An operand that is k-contiguous in memory is staged with 16-byte row loads;
+// one that is m- (or n-) contiguous is loaded 4 k-rows x 8 columns per thread and transposed
+// in registers on the way into LDS, its k positions rotated per 8-row group so that those
+// transposed writes spread over the banks.
+
+#include "matmul.h"
+
+namespace limn {
+namespace {
+
+constexpr int MM_THREADS = 256;
+constexpr int BK = 64;
+constexpr int LS = BK + 8;  // LDS row stride (elements) of both operand tiles
+
+__device__ __forceinline__ u16x8 zero8() {
+  u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+  return z;
+}
+
+// k position of element k in LDS row `row` of an operand staged from row-contiguous memory:
+// rotated by 8 per 8-row group (identity for k-contiguous staging).
+template <bool KCONTIG>
+__device__ __forceinline__ int kpos(int row, int k) {
+  return KCONTIG ? k : ((k + 8 * ((row >> 3) & 7)) & (BK - 1));
+}
+
+// One operand's stage: ROWS (m or n) x BK values, staged into an LDS tile [row][k].
+//   KCONTIG: memory is k-contiguous: element (row, k) at base + row*stride + k.
+//   else   : memory is row-contiguous: element (row, k) at base + k*stride + row.
+template <int ROWS, bool KCONTIG>
+struct OperandStage {
+  static constexpr int LOADS = ROWS * BK / 8 / MM_THREADS;  // 16-byte loads per thread
+  u16x8 r[LOADS];
+
+  __device__ __forceinline__ void load(const u16* base, int64_t row0, int64_t rows, int64_t k0, int64_t depth,
+                                       int64_t stride) {
+    if (KCONTIG) {
+#pragma unroll
+      for (int s = 0; s < LOADS; s++) {
+        const int c = threadIdx.x + s * MM_THREADS;
+        const int row = c / (BK / 8), kc = c % (BK / 8);
+        const int64_t gr = row0 + row, gk = k0 + kc * 8;
+        r[s] = (gr < rows && gk < depth) ? *(const u16x8*)(base + gr * stride + gk) : zero8();
+      }
+    } else {
+      // a block is 4 k-rows x 8 columns; column chunks vary fastest across lanes (coalesced)
+#pragma unroll
+      for (int s = 0; s < LOADS / 4; s++) {
+        const int blk = threadIdx.x + s * MM_THREADS;
+        const int rc = blk % (ROWS / 8), kg = blk / (ROWS / 8);
+        const int64_t gr = row0 + rc * 8;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int64_t gk = k0 + kg * 4 + e;
+          r[4 * s + e] = (gr < rows && gk < depth) ? *(const u16x8*)(base + gk * stride + gr) : zero8();
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(u16* lds) {
+    if (KCONTIG) {
+#pragma unroll
+      for (int s = 0; s < LOADS; s++) {
+        const int c = threadIdx.x + s * MM_THREADS;
+        const int row = c / (BK / 8), kc = c % (BK / 8);
+        *(u16x8*)(lds + row * LS + kc * 8) = r[s];
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < LOADS / 4; s++) {
+        const int blk = threadIdx.x + s * MM_THREADS;
+        const int rc = blk % (ROWS / 8), kg = blk / (ROWS / 8);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+          u16x4 t = {r[4 * s][c], r[4 * s + 1][c], r[4 * s + 2][c], r[4 * s + 3][c]};
+          const int row = rc * 8 + c;
+          *(u16x4*)(lds + row * LS + kpos<false>(row, kg * 4)) = t;
+        }
+      }
+    }
+  }
+};
+
+template <typename T, int BM, int BN, bool A_K, bool B_K, int EPI>
+__global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restrict__ a, const u16* __restrict__ b,
+                                                             u16* __restrict__ c, MatmulShape s) {
+  constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 accumulators per wave along m and n
+  __shared__ __attribute__((aligned(16))) u16 As[2][BM * LS];
+  __shared__ __attribute__((aligned(16))) u16 Bs[2][BN * LS];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, n32 = lane & 31;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t tiles_n = (s.N + BN - 1) / BN, tiles_m = (s.M + BM - 1) / BM;
+  const int64_t per_batch = tiles_m * tiles_n;
+  const int64_t bz = blockIdx.x / per_batch;
+  const int64_t t = blockIdx.x - bz * per_batch;
+  const int64_t tm = t / tiles_n, tn = t - tm * tiles_n;
+  const int64_t m0 = tm * BM, n0 = tn * BN;
+  const u16* abase = a + bz * s.a_batch;
+  const u16* bbase = b + bz * s.b_batch;
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+
+  OperandStage<BM, A_K> sa;
+  OperandStage<BN, B_K> sb;
+  const int64_t a_stride = A_K ? s.a_m : s.a_k;
+  const int64_t b_stride = B_K ? s.b_n : s.b_k;
+  const int stages = (int)((s.K + BK - 1) / BK);
+  sa.load(abase, m0, s.M, 0, s.K, a_stride);
+  sb.load(bbase, n0, s.N, 0, s.K, b_stride);
+  sa.store(As[0]);
+  sb.store(Bs[0]);
+  __syncthreads();
+  for (int st = 0; st < stages; st++) {
+    const int cur = st & 1;
+    if (st + 1 < stages) {
+      sa.load(abase, m0, s.M, (int64_t)(st + 1) * BK, s.K, a_stride);
+      sb.load(bbase, n0, s.N, (int64_t)(st + 1) * BK, s.K, b_stride);
+    }
+    const u16* at = As[cur];
+    const u16* bt = Bs[cur];
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; kk++) {
+      u16x8 av[TM], bv[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const int row = wm * (BM / 2) + i * 32 + n32;
+        av[i] = *(const u16x8*)(at + row * LS + kpos<A_K>(row, kk * 16 + 8 * h));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int row = wn * (BN / 2) + j * 32 + n32;
+        bv[j] = *(const u16x8*)(bt + row * LS + kpos<B_K>(row, kk * 16 + 8 * h));
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = T::mfma32(av[i], bv[j], acc[i][j]);
+    }
+    if (st + 1 < stages) {
+      sa.store(As[cur ^ 1]);
+      sb.store(Bs[cur ^ 1]);
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane holds rows 8*(e/4) + 4h + e%4 of each 32x32 tile, column n32
+  u16* cbase = c + bz * s.c_batch;
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int64_t col = n0 + wn * (BN / 2) + j * 32 + n32;
+      if (col >= s.N) continue;
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int64_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (row < s.M) {
+          float v = acc[i][j][e];
+          if (EPI == MATMUL_EPILOGUE_RELU) v = v > 0.f ? v : 0.f;
+          cbase[row * s.c_m + col * s.c_n] = T::pack(v);
+        }
+      }
+    }
+}
+
+template <typename T, int BM, int BN, bool A_K, bool B_K>
+int launch_tile(const void* a, const void* b, void* c, const MatmulShape& s, int epilogue, hipStream_t stream) {
+  const int64_t blocks = s.batch * ((s.M + BM - 1) / BM) * ((s.N + BN - 1) / BN);
+  if (blocks > 0x7fffffff) return fail(LIMN_HIP_EUNSUPPORTED, "matmul: %lld workgroups exceed one launch", (long long)blocks);
+  const dim3 grid((unsigned)blocks), block(MM_THREADS);
+  if (epilogue == MATMUL_EPILOGUE_RELU)
+    hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, MATMUL_EPILOGUE_RELU>), grid, block, 0, stream,
+                       (const u16*)a, (const u16*)b, (u16*)c, s);
+  else
+    hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, MATMUL_EPILOGUE_NONE>), grid, block, 0, stream,
+                       (const u16*)a, (const u16*)b, (u16*)c, s);
+  return check_hip(hipGetLastError(), "launching the matmul kernel");
+}
+
+// 256 x 256 tiles when they still give every compute unit a workgroup, else 128 x 128.
+template <typename T, bool A_K, bool B_K>
+int launch_layout(const void* a, const void* b, void* c, const MatmulShape& s, int epilogue, hipStream_t stream) {
+  const int64_t big = s.batch * ((s.M + 255) / 256) * ((s.N + 255) / 256);
+  if (big >= 256) return launch_tile<T, 256, 256, A_K, B_K>(a, b, c, s, epilogue, stream);
+  return launch_tile<T, 128, 128, A_K, B_K>(a, b, c, s, epilogue, stream);
+}
+
+template <typename T>
+int launch_type(const void* a, const void* b, void* c, const MatmulShape& s, int epilogue, hipStream_t stream) {
+  const bool a_k = s.a_k == 1, b_k = s.b_k == 1;
+  if (a_k && b_k) return launch_layout<T, true, true>(a, b, c, s, epilogue, stream);
+  if (a_k) return launch_layout<T, true, false>(a, b, c, s, epilogue, stream);
+  if (b_k) return launch_layout<T, false, true>(a, b, c, s, epilogue, stream);
+  return launch_layout<T, false, false>(a, b, c, s, epilogue, stream);
+}
+
+}  // namespace
+
+int matmul_layout_ok(const MatmulShape& s) {
+  // one of the two strides of each operand must be 1, the other a multiple of 8 elements, so
+  // every 16-byte load is aligned; the contiguous extent must be a multiple of 8 so that a
+  // 16-byte chunk never straddles the end of a row
+  const bool a_ok = (s.a_k == 1 && s.a_m % 8 == 0 && s.K % 8 == 0) || (s.a_m == 1 && s.a_k % 8 == 0 && s.M % 8 == 0);
+  const bool b_ok = (s.b_k == 1 && s.b_n % 8 == 0 && s.K % 8 == 0) || (s.b_n == 1 && s.b_k % 8 == 0 && s.N % 8 == 0);
+  const bool batch_ok = s.a_batch % 8 == 0 && s.b_batch % 8 == 0;
+  return a_ok && b_ok && batch_ok;
+}
+
+int launch_matmul(const void* a, const void* b, void* c, int dtype, const MatmulShape& s, int epilogue, hipStream_t stream) {
+  if (dtype == LIMN_HIP_BFLOAT16) return launch_type<BF16>(a, b, c, s, epilogue, stream);
+  return launch_type<F16>(a, b, c, s, epilogue, stream);
+}
+
+}  // namespace limn

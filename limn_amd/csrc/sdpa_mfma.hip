@@ -47,6 +47,12 @@ __device__ __forceinline__ int tpos(int r) {
   return (r & ~31) | (gp << 2) | (r & 3);
 }
 
+// A transposed tile's row `d` stores its TILE positions rotated by 8 * ((d >> 3) & 7): the
+// staging writes 8 rows apart then land in 8 different 16-byte bank groups, while an MFMA
+// operand read (8 consecutive positions starting at a multiple of 8, one row per lane)
+// stays one contiguous 16-byte word.
+__device__ __forceinline__ int trot(int d, int pos) { return (pos + 8 * ((d >> 3) & 7)) & (TILE - 1); }
+
 __device__ __forceinline__ u16x8 zero8() {
   u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
   return z;
@@ -108,7 +114,8 @@ struct Stage {
 #pragma unroll
           for (int c = 0; c < 8; c++) {
             u16x4 t = {r[s][0][c], r[s][1][c], r[s][2][c], r[s][3][c]};
-            *(u16x4*)(cols + (col * 8 + c) * CS + p) = t;
+            const int d = col * 8 + c;
+            *(u16x4*)(cols + d * CS + trot(d, p)) = t;
           }
         }
       }
@@ -233,7 +240,8 @@ __global__ __launch_bounds__(THREADS, 2) void sdpa_fwd_mfma(const u16* __restric
         for (int j = 0; j < 8; j++) pb[j] = T::pack(s[sub][8 * c + j]);
 #pragma unroll
         for (int dt = 0; dt < D / 32; dt++) {
-          const u16x8 a = *(const u16x8*)(Vt + (dt * 32 + n) * CS + sub * 32 + 16 * c + 8 * h);
+          const int d = dt * 32 + n;
+          const u16x8 a = *(const u16x8*)(Vt + d * CS + trot(d, sub * 32 + 16 * c + 8 * h));
           acc[dt] = T::mfma32(a, pb, acc[dt]);
         }
       }
@@ -334,7 +342,8 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_q_mfma(const u16* __restr
         for (int j = 0; j < 8; j++) g[j] = T::pack(s[sub][8 * c + j]);
 #pragma unroll
         for (int dt = 0; dt < D / 32; dt++) {
-          const u16x8 a = *(const u16x8*)(Kt + (dt * 32 + n) * CS + sub * 32 + 16 * c + 8 * h);
+          const int d = dt * 32 + n;
+          const u16x8 a = *(const u16x8*)(Kt + d * CS + trot(d, sub * 32 + 16 * c + 8 * h));
           acc[dt] = T::mfma32(a, g, acc[dt]);
         }
       }
@@ -448,9 +457,10 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_mfma(const u16* __rest
         }
 #pragma unroll
         for (int dt = 0; dt < D / 32; dt++) {
-          const u16x8 a = *(const u16x8*)(Ot + (dt * 32 + n) * CS + sub * 32 + 16 * c + 8 * h);
+          const int d = dt * 32 + n, pos = trot(d, sub * 32 + 16 * c + 8 * h);
+          const u16x8 a = *(const u16x8*)(Ot + d * CS + pos);
           gv[dt] = T::mfma32(a, pb, gv[dt]);
-          const u16x8 e = *(const u16x8*)(Qt + (dt * 32 + n) * CS + sub * 32 + 16 * c + 8 * h);
+          const u16x8 e = *(const u16x8*)(Qt + d * CS + pos);
           gk[dt] = T::mfma32(e, gb, gk[dt]);
         }
       }

@@ -290,12 +290,105 @@ class Launch:
 
 @dataclass
 class Planned:
-    """What one nest became: kernels to launch in order, and the scratch bytes they share."""
+    """What one nest became: kernels to launch in order, and the scratch bytes they share; or a
+    dense contraction handed to liblimn_hip.so's MFMA kernel (`contraction`)."""
 
     source: str
     launches: list[Launch]
     scratch_bytes: int = 0
     notes: dict = field(default_factory=dict)
+    contraction: "Contraction | None" = None
+
+
+@dataclass(frozen=True)
+class Contraction:
+    """A SUM nest that is c[b, m, n] = sum_k a[b, m, k] * b[b, k, n] over two input buffers, with
+    every stride in elements (the arguments of limn_hip_matmul)."""
+
+    a_input: int
+    b_input: int
+    a_offset: int
+    b_offset: int
+    dtype: DType
+    batch: int
+    M: int
+    N: int
+    K: int
+    a_batch: int
+    a_m: int
+    a_k: int
+    b_batch: int
+    b_k: int
+    b_n: int
+    c_batch: int
+    c_m: int
+    c_n: int
+
+
+def _flat_stride(coeffs: dict[str, int], batch_vars: list[tuple[str, int]]) -> int | None:
+    """One stride for the row-major flattening of the batch vars, if the operand's coefficients
+    allow it (all zero is a broadcast: stride 0)."""
+    if not batch_vars:
+        return 0
+    stride = coeffs.get(batch_vars[-1][0], 0)
+    expect = stride
+    for j in range(len(batch_vars) - 1, 0, -1):
+        expect = expect * batch_vars[j][1]
+        if coeffs.get(batch_vars[j - 1][0], 0) != expect:
+            return None
+    return stride
+
+
+def find_contraction(nest: LoopNest, shape: NestShape) -> Contraction | None:
+    """The dense-contraction reading of a reduce nest (reference limn/cuda_emit.py:376-505
+    detects the same shape): one reduce var, a body of exactly two unmasked loads and their
+    product, each load depending on the reduce var, the batch vars and one row var of its own."""
+    if shape.fold is not Op.ADD or len(shape.inner) != 1 or len(shape.body) != 3:
+        return None
+    loads = [i for i in shape.body if i.opcode is Opcode.LOAD]
+    mul = [i for i in shape.body if i.opcode is Opcode.ARITH and i.arg is Op.MUL]
+    if len(loads) != 2 or len(mul) != 1 or shape.item != mul[0].dest or set(mul[0].srcs) != {loads[0].dest, loads[1].dest}:
+        return None
+    if any(l.arg[2].bounds for l in loads):
+        return None
+    dtype = loads[0].value_type
+    if dtype not in (bfloat16, float16) or loads[1].value_type != dtype or shape.reduce_dtype != dtype:
+        return None
+    if nest.kernel.target.dtype != dtype:
+        return None
+    r, K = shape.inner[0]
+    kept = sorted(shape.outer, key=lambda ve: int(ve[0][1:]))
+    ta, tb = dict(loads[0].arg[1].terms), dict(loads[1].arg[1].terms)
+    if r not in ta or r not in tb:
+        return None
+    only_a = [v for v, _ in kept if v in ta and v not in tb]
+    only_b = [v for v, _ in kept if v in tb and v not in ta]
+    if not only_a or not only_b:
+        return None
+    m_var, n_var = only_a[-1], only_b[-1]  # the row dims come after any batch dims an operand broadcasts
+    extent = dict(kept)
+    batch_vars = [(v, e) for v, e in kept if v not in (m_var, n_var)]
+    tc = dict(shape.out_index.terms)
+    if tc.get(m_var, 0) == 0 or tc.get(n_var, 0) == 0 or shape.out_index.const != 0:
+        return None
+    a_b, b_b, c_b = (_flat_stride(t, batch_vars) for t in (ta, tb, tc))
+    if a_b is None or b_b is None or c_b is None:
+        return None
+    batch = math.prod(e for _, e in batch_vars)
+    M, N = extent[m_var], extent[n_var]
+    a_in, b_in = int(loads[0].arg[0][2:]), int(loads[1].arg[0][2:])
+    a_m, a_k, b_n, b_k = ta[m_var], ta[r], tb[n_var], tb[r]
+    c_m, c_n = tc[m_var], tc[n_var]
+    if batch > 1 and b_b == 0 and a_b == M * a_m and c_b == M * c_m:
+        M, batch, a_b, c_b = M * batch, 1, 0, 0  # a shared right operand: one taller contraction
+    con = Contraction(a_in, b_in, loads[0].arg[1].const, loads[1].arg[1].const, dtype, batch, M, N, K, a_b, a_m, a_k, b_b, b_k, b_n, c_b, c_m, c_n)
+    if con.a_offset % 8 or con.b_offset % 8:
+        return None
+    from limn_amd.dtypes import ABI_CODE
+
+    lib = runtime.kernels()
+    ok = lib.limn_hip_matmul_supported(ABI_CODE[dtype], M, N, K, a_b, a_m, a_k, b_b, b_k, b_n)
+    return con if ok else None
 
 
 def _vec_width(nest_shape: NestShape, bufs: Buffers, var: str, extent: int) -> int:
@@ -510,6 +603,9 @@ def plan_nest(nest: LoopNest) -> Planned:
     shape = read_nest(nest)
     if shape.fold is None:
         return plan_elementwise(nest, shape, bufs)
+    con = find_contraction(nest, shape)
+    if con is not None:
+        return Planned("", [], contraction=con, notes={"mfma": True})
     return plan_reduce(nest, shape, bufs)
 
 
@@ -531,11 +627,13 @@ def _launcher(dev, fn: int, launch: Launch, nin: int):
 def nest_runners(dev, nests: list[LoopNest]):
     """Compile every nest of a plan into one hipRTC program; one runner per nest, in order."""
     plans = [plan_nest(n) for n in nests]
-    source = PRELUDE + "\n".join(p.source for p in plans)
     names = [launch.name for p in plans for launch in p.launches]
-    functions = runtime.load_functions(source, names)
+    functions = runtime.load_functions(PRELUDE + "\n".join(p.source for p in plans), names) if names else {}
     runners = []
     for nest, plan in zip(nests, plans):
+        if plan.contraction is not None:
+            runners.append(_contraction_runner(dev, plan.contraction))
+            continue
         nin = len(nest.kernel.inputs)
         launchers = []
         for launch in plan.launches:
@@ -543,6 +641,22 @@ def nest_runners(dev, nests: list[LoopNest]):
             launchers.append((launch.args, _launcher(dev, functions[launch.name], launch, count - 1)))
         runners.append(_make_runner(dev, launchers, plan.scratch_bytes))
     return runners
+
+
+def _contraction_runner(dev, con: Contraction):
+    from limn_amd.dtypes import ABI_CODE
+
+    lib = dev.lib
+    code = ABI_CODE[con.dtype]
+    size = con.dtype.itemsize
+    tail = (code, con.batch, con.M, con.N, con.K, con.a_batch, con.a_m, con.a_k, con.b_batch, con.b_k, con.b_n, con.c_batch, con.c_m, con.c_n, 0, None)
+
+    def run(inputs: list, outs: list) -> None:
+        a = inputs[con.a_input].ptr + con.a_offset * size
+        b = inputs[con.b_input].ptr + con.b_offset * size
+        runtime.check_limn(lib.limn_hip_matmul(a, b, outs[0].ptr, *tail))
+
+    return run
 
 
 def _make_runner(dev, launchers, scratch_bytes: int):

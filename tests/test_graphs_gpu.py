@@ -263,3 +263,83 @@ def test_config2_full_size(hipdev):
     limn_device.set_device("numpy")
     want = chain(Tensor(x_host[rows])).numpy()
     np.testing.assert_allclose(out[rows], want, rtol=1e-5, atol=1e-5)
+
+
+# ---- dense contractions on matrix cores ----
+
+
+def _plans(dev, t):
+    """The emitter's plan for each nest of t's graph (which kernel family each nest got)."""
+    from limn_amd.codegen import lower_all
+    from limn_amd.hip.emit import plan_nest
+
+    return [plan_nest(n) for n in lower_all([t.node])]
+
+
+@pytest.mark.parametrize(
+    "a_shape,b_shape,ta,tb",
+    [
+        ((64, 32), (32, 48), False, False),
+        ((100, 40), (40, 72), False, False),
+        ((136, 208), (208, 264), False, False),
+        ((40, 24), (40, 56), True, False),
+        ((24, 64), (56, 64), False, True),
+        ((64, 24), (56, 64), True, True),
+        ((3, 33, 16), (3, 16, 40), False, False),
+        ((4, 17, 32), (32, 24), False, False),
+    ],
+    ids=["square", "ragged", "multi-stage", "a-transposed", "b-transposed", "both-transposed", "batched", "broadcast"],
+)
+@pytest.mark.parametrize("dtype", [bfloat16, float16], ids=str)
+def test_contraction_on_mfma(hipdev, a_shape, b_shape, ta, tb, dtype):
+    a_data = rng.standard_normal(a_shape).astype(np.float32)
+    b_data = rng.standard_normal(b_shape).astype(np.float32)
+    a, b = Tensor(a_data, dtype=dtype), Tensor(b_data, dtype=dtype)
+    if ta:
+        a = a.transpose()
+    if tb:
+        b = b.transpose()
+    out = a @ b
+    assert any(p.contraction is not None for p in _plans(hipdev, out)), "the contraction did not reach the MFMA kernel"
+    from limn_amd.dtypes import from_storage, to_storage
+
+    got = from_storage(hipdev.copyout(hipdev.execute([out.node])[0]), dtype, out.shape).astype(np.float64)
+    # the exact answer on the stored operand values (products are exact in f32; one rounding at
+    # the store): the kernel may differ by accumulation order and that final rounding
+    av = from_storage(to_storage(a_data, dtype).view(np.uint8), dtype, a_shape).astype(np.float64)
+    bv = from_storage(to_storage(b_data, dtype).view(np.uint8), dtype, b_shape).astype(np.float64)
+    av = np.swapaxes(av, -1, -2) if ta else av
+    bv = np.swapaxes(bv, -1, -2) if tb else bv
+    exact = av @ bv
+    ulp = 2.0**-8 if dtype is bfloat16 else 2.0**-11
+    np.testing.assert_allclose(got, exact, rtol=2 * ulp, atol=1e-3)
+    # and the numpy oracle, which rounds every half-width product before summing: its error
+    # grows like sqrt(K) rounding steps
+    k = a.shape[-1]
+    check(hipdev, out, rtol=2e-2, atol=4 * ulp * np.sqrt(k) * 2)
+
+
+def test_contraction_falls_back_when_unaligned(hipdev):
+    """K = 13 leaves 16-byte rows misaligned: the general reduce kernels take it."""
+    a, b = Tensor(randf(20, 13), dtype=bfloat16), Tensor(randf(13, 9), dtype=bfloat16)
+    out = a @ b
+    assert all(p.contraction is None for p in _plans(hipdev, out))
+    check(hipdev, out, rtol=2e-2, atol=5e-2)
+
+
+def test_config3_full_size(hipdev):
+    """bf16 A(4096x4096) @ B(4096x4096), f32 accumulate, relu, bf16 store.
+    A, B ~ N(0, 0.125^2) from default_rng(3) (variance 1/sqrt(4096)). Checked against the f32
+    closed form np.matmul on the same bf16 values, then relu and round to bf16."""
+    from limn_amd.dtypes import bf16_bits, bf16_values
+
+    n = 4096
+    r = np.random.default_rng(3)
+    a_vals = bf16_values(bf16_bits((r.standard_normal((n, n), dtype=np.float32) * 0.125)))
+    b_vals = bf16_values(bf16_bits((r.standard_normal((n, n), dtype=np.float32) * 0.125)))
+    limn_device.active_device = hipdev
+    out = (Tensor(a_vals, dtype=bfloat16) @ Tensor(b_vals, dtype=bfloat16)).relu()
+    assert any(p.contraction is not None for p in _plans(hipdev, out))
+    got = out.numpy()
+    want = bf16_values(bf16_bits(np.maximum(a_vals @ b_vals, 0.0)))
+    np.testing.assert_allclose(got, want, rtol=2e-2, atol=2e-2)
