@@ -63,7 +63,7 @@ static int validate(SdpaPass pass, const SdpaArgs& a) {
 static int run(SdpaPass pass, const SdpaArgs& a) {
   const int rc = validate(pass, a);
   if (rc != LIMN_HIP_OK) return rc;
-  if (mfma_supports(a.dtype, a.hd, a.hd_v)) return launch_sdpa_mfma(pass, a);
+  if (mfma_supports(a.dtype, a.hd, a.hd_v) && mfma_fits(a.t_q, a.t_k, a.hd)) return launch_sdpa_mfma(pass, a);
   if (rows_supports(a.dtype, a.hd, a.hd_v)) return launch_sdpa_rows(pass, a);
   return fail(LIMN_HIP_EUNSUPPORTED, "%s: no kernel for head dims %lld and %lld (at most 256)", pass_name(pass),
               (long long)a.hd, (long long)a.hd_v);

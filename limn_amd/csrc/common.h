@@ -15,6 +15,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef u16 u16x8 __attribute__((ext_vector_type(8)));
 typedef u16 u16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // ---- storage <-> compute conversions --------------------------------------------------------
 // bfloat16 and float16 are storage widths: they are widened to float to compute and rounded
@@ -54,6 +58,11 @@ struct BF16 {
   static __device__ __forceinline__ f32x16 mfma32(u16x8 a, u16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  // two floats rounded into one 32-bit word, the first in the low half (v_cvt_pk_bf16_f32)
+  static __device__ __forceinline__ unsigned pack2(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf16x2));
+  }
 };
 struct F16 {
   typedef u16 Storage;
@@ -65,7 +74,20 @@ struct F16 {
   static __device__ __forceinline__ f32x16 mfma32(u16x8 a, u16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
+  static __device__ __forceinline__ unsigned pack2(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(v, f16x2));
+  }
 };
+
+// Items base .. base+7 of an accumulator, rounded to the storage width and packed in order: the
+// 16-byte MFMA operand they form.
+template <typename T>
+__device__ __forceinline__ u16x8 pack8(const f32x16& s, int base) {
+  const u32x4 w = {T::pack2(s[base], s[base + 1]), T::pack2(s[base + 2], s[base + 3]), T::pack2(s[base + 4], s[base + 5]),
+                   T::pack2(s[base + 6], s[base + 7])};
+  return __builtin_bit_cast(u16x8, w);
+}
 
 // The width row statistics (L, delta) are kept at: float for the half widths, else the dtype.
 template <typename T>

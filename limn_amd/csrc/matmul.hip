@@ -106,7 +106,7 @@ __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restri
   __shared__ __attribute__((aligned(16))) u16 As[2][BM * LS];
   __shared__ __attribute__((aligned(16))) u16 Bs[2][BN * LS];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, n32 = lane & 31;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n32 = lane & 31;
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t tiles_n = (s.N + BN - 1) / BN, tiles_m = (s.M + BM - 1) / BM;
   const int64_t per_batch = tiles_m * tiles_n;

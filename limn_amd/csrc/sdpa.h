@@ -27,6 +27,7 @@ enum SdpaPass { SDPA_FWD = 0, SDPA_BWD_Q = 1, SDPA_BWD_KV = 2 };
 
 // MFMA flash kernels: bf16/f16, hd == hd_v in {64, 128}.
 bool mfma_supports(int dtype, int64_t hd, int64_t hd_v);
+bool mfma_fits(int64_t t_q, int64_t t_k, int64_t hd);
 int launch_sdpa_mfma(SdpaPass pass, const SdpaArgs& a);
 
 // General-width kernels: any float dtype, max(hd, hd_v) <= 256.

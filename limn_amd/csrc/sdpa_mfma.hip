@@ -4,10 +4,12 @@
 // 679-714), each deterministic: every total is accumulated inside one wave in a fixed order.
 //
 // Work decomposition (all three kernels):
-//   a workgroup is 4 waves and owns BLOCK_ROWS = 128 *resident* rows (queries for the forward
-//   and dQ pass, keys for the dK/dV pass), 32 per wave; the other side *streams* past in tiles
-//   of TILE = 64 rows staged through LDS, the next tile's global loads in flight while the
-//   current one is computed.
+//   a workgroup is 4 waves and owns 128 * NT *resident* rows (queries for the forward and dQ
+//   pass, keys for the dK/dV pass), NT tiles of 32 per wave; the other side *streams* past in
+//   tiles of TILE = 64 rows staged through LDS (the next tile's global loads in flight while the
+//   current one is computed) and is consumed 32 streamed rows at a time. Each operand fragment
+//   read from LDS feeds NT MFMAs, one per resident tile: at NT = 1 one 1 KB read per MFMA
+//   would ask LDS for its full bandwidth just to keep the matrix cores fed.
 //
 // Orientation. Every product is v_mfma_f32_32x32x16_{bf16,f16} with the resident rows on the
 // N side, so each lane owns one resident row (n = lane % 32) and its score column is spread
@@ -32,7 +34,6 @@ namespace {
 
 constexpr int WAVES = 4;
 constexpr int THREADS = 64 * WAVES;
-constexpr int BLOCK_ROWS = 32 * WAVES;
 constexpr int TILE = 64;
 constexpr float LOG2E = 1.4426950408889634f;
 
@@ -65,6 +66,19 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
+// A (rows x D) row-major matrix of one head, read through a buffer resource: the hardware
+// bounds check returns zeros for rows past the end, so loads need no branches.
+struct Rows {
+  __amdgpu_buffer_rsrc_t rsrc;
+  __device__ __forceinline__ Rows(const u16* base, int rows, int width) {
+    rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, rows * width * 2, 0x00020000);
+  }
+  // 8 elements starting at element `offset` (zeros when past the end)
+  __device__ __forceinline__ u16x8 load8(int offset) const {
+    return __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset * 2, 0, 0));
+  }
+};
+
 // Global -> registers -> LDS staging of one or two TILE x D row-major tiles. Each participating
 // thread carries a 4-row x 8-column block, so it can write its rows (16 B per row) into a
 // row-major LDS tile and its columns (8 B per column, 4 rows) into a transposed one.
@@ -75,21 +89,17 @@ struct Stage {
   static constexpr int SLOTS = (2 * PER_TILE + THREADS - 1) / THREADS;  // both tiles
   u16x8 r[SLOTS][4];
 
-  // Load tile `which` (0 or 1) of a pair: rows [row0, row0 + TILE) of base (rows x D), zero
-  // past `rows`.
-  __device__ __forceinline__ void load(const u16* base0, const u16* base1, int64_t row0, int64_t rows) {
+  // rows [row0, row0 + TILE) of both matrices; rows past their end read as zeros
+  __device__ __forceinline__ void load(const Rows& m0, const Rows& m1, int row0) {
 #pragma unroll
     for (int s = 0; s < SLOTS; s++) {
       const int idx = threadIdx.x + s * THREADS;
       if (idx < 2 * PER_TILE) {
         const int which = idx / PER_TILE, w = idx - which * PER_TILE;
         const int col = w % COLS, grp = w / COLS;
-        const u16* base = which ? base1 : base0;
+        const Rows& m = which ? m1 : m0;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int64_t row = row0 + grp * 4 + e;
-          r[s][e] = row < rows ? *(const u16x8*)(base + row * D + col * 8) : zero8();
-        }
+        for (int e = 0; e < 4; e++) r[s][e] = m.load8((row0 + grp * 4 + e) * D + col * 8);
       }
     }
   }
@@ -126,7 +136,7 @@ struct Stage {
 // acc (32 rows x 32 cols per tile, row = dim d, col = resident row n) -> global (rows, D),
 // scaled by `mul`, for the lane's resident row `row` if it is < rows.
 template <typename T, int D>
-__device__ __forceinline__ void store_transposed(u16* base, const f32x16* acc, int64_t row, int64_t rows, float mul) {
+__device__ __forceinline__ void store_transposed(u16* base, const f32x16* acc, int row, int rows, float mul) {
   if (row >= rows) return;
   const int h = (threadIdx.x >> 5) & 1;
 #pragma unroll
@@ -140,228 +150,275 @@ __device__ __forceinline__ void store_transposed(u16* base, const f32x16* acc, i
   }
 }
 
-// ---------------------------------------------------------------------------------------------
-// Forward.
-template <typename T, int D, bool CAUSAL, bool MASK>
-__global__ __launch_bounds__(THREADS, 2) void sdpa_fwd_mfma(const u16* __restrict__ q, const u16* __restrict__ k,
-                                                            const u16* __restrict__ v, const u16* __restrict__ mask,
-                                                            u16* __restrict__ out, float* __restrict__ lse, int64_t batch,
-                                                            int64_t t_q, int64_t t_k, float scale) {
-  constexpr int RS = D + 8, CS = TILE + 8;
-  __shared__ __attribute__((aligned(16))) u16 Ks[TILE * RS];
-  __shared__ __attribute__((aligned(16))) u16 Vt[D * CS];
-  __shared__ float Mk[TILE];
+// The streamed-key mask of one 32-key half, as item-ordered float4s: mk[g][e] belongs to key
+// offset sub * 32 + 8 * g + 4 * h + e, the key of accumulator item 4 * g + e.
+__device__ __forceinline__ void read_mask(const float* Mk, int sub, int h, f32x4 (&mk)[4]) {
+#pragma unroll
+  for (int g = 0; g < 4; g++) mk[g] = *(const f32x4*)(Mk + sub * 32 + 8 * g + 4 * h);
+}
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, n = lane & 31;
-  const int64_t nqb = (t_q + BLOCK_ROWS - 1) / BLOCK_ROWS;
-  const int64_t b = blockIdx.x % batch;
-  const int64_t qb = nqb - 1 - blockIdx.x / batch;  // causal: the longest rows go first
-  const int64_t q0 = qb * BLOCK_ROWS, wq0 = q0 + wave * 32, row = wq0 + n;
-  const u16* qbase = q + b * t_q * D;
-  const u16* kbase = k + b * t_k * D;
-  const u16* vbase = v + b * t_k * D;
-  const float c2 = scale * LOG2E;
-
-  u16x8 qf[D / 16];
-#pragma unroll
-  for (int ds = 0; ds < D / 16; ds++) qf[ds] = row < t_q ? *(const u16x8*)(qbase + row * D + ds * 16 + 8 * h) : zero8();
-
-  f32x16 acc[D / 32];
-#pragma unroll
-  for (int dt = 0; dt < D / 32; dt++) acc[dt] = zero16();
-  float m = neg_inf(), l = 0.f;
-
-  const int64_t kend = CAUSAL ? (q0 + BLOCK_ROWS < t_k ? q0 + BLOCK_ROWS : t_k) : t_k;
-  const int ntiles = (int)((kend + TILE - 1) / TILE);
-  Stage<D> st;
-  st.load(kbase, vbase, 0, t_k);
-  for (int it = 0; it < ntiles; it++) {
-    const int64_t k0 = (int64_t)it * TILE;
-    if (it > 0) __syncthreads();
-    st.store(Ks, nullptr, nullptr, Vt);
-    if (MASK && threadIdx.x < TILE) {
-      const int64_t key = k0 + threadIdx.x;
-      Mk[threadIdx.x] = key < t_k ? T::unpack(mask[b * t_k + key]) : 0.f;
-    }
-    __syncthreads();
-    if (it + 1 < ntiles) st.load(kbase, vbase, k0 + TILE, t_k);
-    if (CAUSAL && k0 > wq0 + 31) continue;  // every key of this tile is right of this wave's rows
-
-    f32x16 s[2];
-#pragma unroll
-    for (int sub = 0; sub < 2; sub++) {
-      s[sub] = zero16();
-#pragma unroll
-      for (int ds = 0; ds < D / 16; ds++) {
-        const u16x8 a = *(const u16x8*)(Ks + (sub * 32 + n) * RS + ds * 16 + 8 * h);
-        s[sub] = T::mfma32(a, qf[ds], s[sub]);
-      }
-    }
-    const bool edge = (k0 + TILE > t_k) || MASK || (CAUSAL && k0 + TILE - 1 > wq0);
-    if (edge) {
-#pragma unroll
-      for (int sub = 0; sub < 2; sub++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-          const int r = sub * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-          const int64_t key = k0 + r;
-          const bool hide = key >= t_k || (CAUSAL && key > row) || (MASK && Mk[r] == 0.f);
-          if (hide) s[sub][i] = neg_inf();
-        }
-    }
-    float mx = neg_inf();
-#pragma unroll
-    for (int sub = 0; sub < 2; sub++)
-#pragma unroll
-      for (int i = 0; i < 16; i++) mx = fmaxf(mx, s[sub][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mnew = fmaxf(m, mx);
-    const float base = mnew == neg_inf() ? 0.f : mnew * c2;
-    const float alpha = fast_exp2(m * c2 - base);
-    float rs = 0.f;
-#pragma unroll
-    for (int sub = 0; sub < 2; sub++)
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const float p = fast_exp2(fmaf(s[sub][i], c2, -base));
-        s[sub][i] = p;
-        rs += p;
-      }
-    l = fmaf(l, alpha, rs);
-    m = mnew;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; dt++) acc[dt] *= alpha;
-#pragma unroll
-    for (int sub = 0; sub < 2; sub++)
-#pragma unroll
-      for (int c = 0; c < 2; c++) {
-        u16x8 pb;
-#pragma unroll
-        for (int j = 0; j < 8; j++) pb[j] = T::pack(s[sub][8 * c + j]);
-#pragma unroll
-        for (int dt = 0; dt < D / 32; dt++) {
-          const int d = dt * 32 + n;
-          const u16x8 a = *(const u16x8*)(Vt + d * CS + trot(d, sub * 32 + 16 * c + 8 * h));
-          acc[dt] = T::mfma32(a, pb, acc[dt]);
-        }
-      }
-  }
-  const float total = l + __shfl_xor(l, 32);
-  store_transposed<T, D>(out + b * t_q * D, acc, row, t_q, 1.f / total);
-  if (h == 0 && row < t_q) lse[b * t_q + row] = m * scale + logf(total);
+// Whether accumulator item i of a 32-key half is a key that `row` may not see: past t_k, right of
+// the row under a causal mask, or zero in the key mask. Bitwise terms on values already in
+// registers, applied by the callers as selects: the short-circuit form, whose LDS read of the mask
+// sat under a branch, was compiled into code that left item 0 visible whatever its mask said.
+template <bool CAUSAL, bool MASK>
+__device__ __forceinline__ bool hidden(int k0, int sub, int i, int h, int t_k, int row, const f32x4 (&mk)[4]) {
+  const int key = k0 + sub * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+  bool hide = key >= t_k;
+  if (CAUSAL) hide |= key > row;
+  if (MASK) hide |= mk[i >> 2][i & 3] == 0.f;
+  return hide;
 }
 
 // ---------------------------------------------------------------------------------------------
-// dQ pass: resident query rows, keys streaming.
-template <typename T, int D, bool CAUSAL, bool MASK>
+// Forward. NT 32-row query tiles per wave: every K or V^T fragment read from LDS feeds NT MFMAs.
+// The 64-key streamed tile is taken 32 keys at a time, one online-softmax step each. A causal
+// half that lies wholly right of a wave's rows is computed anyway and masked to exact zeros:
+// skipping it would branch around the accumulators, and the register allocator answers such a
+// join by copying every accumulator register.
+template <typename T, int D, int NT, bool CAUSAL, bool MASK>
+__global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const u16* __restrict__ q, const u16* __restrict__ k,
+                                                            const u16* __restrict__ v, const u16* __restrict__ mask,
+                                                            u16* __restrict__ out, float* __restrict__ lse, int64_t batch,
+                                                            int t_q, int t_k, float scale) {
+  constexpr int RS = D + 8, CS = TILE + 8, ROWS = 128 * NT;
+  __shared__ __attribute__((aligned(16))) u16 Ks[TILE * RS];
+  __shared__ __attribute__((aligned(16))) u16 Vt[D * CS];
+  __shared__ __attribute__((aligned(16))) float Mk[TILE];
+
+  // the wave index in a scalar register: the per-wave tile bounds and causal tests below are then
+  // uniform branches instead of exec-masked ones
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
+  const int64_t nqb = (t_q + ROWS - 1) / ROWS;
+  const int64_t b = blockIdx.x % batch;
+  const int64_t qb = nqb - 1 - blockIdx.x / batch;  // causal: the longest rows go first
+  const int q0 = (int)qb * ROWS, wq0 = q0 + wave * 32 * NT;
+  const Rows qrows(q + b * (int64_t)t_q * D, t_q, D);
+  const Rows krows(k + b * (int64_t)t_k * D, t_k, D), vrows(v + b * (int64_t)t_k * D, t_k, D);
+  const float c2 = scale * LOG2E;
+
+  u16x8 qf[NT][D / 16];
+  f32x16 acc[NT][D / 32];
+  float m[NT], l[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int row = wq0 + 32 * t + n;
+#pragma unroll
+    for (int ds = 0; ds < D / 16; ds++) qf[t][ds] = qrows.load8(row * D + ds * 16 + 8 * h);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++) acc[t][dt] = zero16();
+    m[t] = neg_inf();
+    l[t] = 0.f;
+  }
+
+  const int kend = CAUSAL ? (q0 + ROWS < t_k ? q0 + ROWS : t_k) : t_k;
+  const int ntiles = (kend + TILE - 1) / TILE;
+  Stage<D> st;
+  st.load(krows, vrows, 0);
+  for (int it = 0; it < ntiles; it++) {
+    const int k0 = it * TILE;
+    if (it > 0) __syncthreads();
+    st.store(Ks, nullptr, nullptr, Vt);
+    if (MASK && threadIdx.x < TILE) {
+      const int key = k0 + threadIdx.x;
+      Mk[threadIdx.x] = key < t_k ? T::unpack(mask[b * (int64_t)t_k + key]) : 0.f;
+    }
+    __syncthreads();
+    if (it + 1 < ntiles) st.load(krows, vrows, k0 + TILE);
+#pragma unroll
+    for (int sub = 0; sub < 2; sub++) {
+      const int s0 = k0 + sub * 32;
+      // every K fragment of this half first, then the MFMA chain: the reads overlap each other
+      u16x8 kfr[D / 16];
+#pragma unroll
+      for (int ds = 0; ds < D / 16; ds++) kfr[ds] = *(const u16x8*)(Ks + (sub * 32 + n) * RS + ds * 16 + 8 * h);
+      f32x16 s[NT];
+#pragma unroll
+      for (int t = 0; t < NT; t++) s[t] = zero16();
+#pragma unroll
+      for (int ds = 0; ds < D / 16; ds++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) s[t] = T::mfma32(kfr[ds], qf[t][ds], s[t]);
+      const bool edge = (s0 + 32 > t_k) || MASK || (CAUSAL && s0 + 31 > wq0);
+      f32x4 mk[4];
+      if (MASK) read_mask(Mk, sub, h, mk);
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const int row = wq0 + 32 * t + n;
+        if (edge) {
+#pragma unroll
+          for (int i = 0; i < 16; i++)
+            s[t][i] = hidden<CAUSAL, MASK>(k0, sub, i, h, t_k, row, mk) ? neg_inf() : s[t][i];
+        }
+        float mx = neg_inf();
+#pragma unroll
+        for (int i = 0; i < 16; i++) mx = fmaxf(mx, s[t][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mnew = fmaxf(m[t], mx);
+        const float base = mnew == neg_inf() ? 0.f : mnew * c2;
+        const float alpha = fast_exp2(m[t] * c2 - base);
+        float rs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const float p = fast_exp2(fmaf(s[t][i], c2, -base));
+          s[t][i] = p;
+          rs += p;
+        }
+        l[t] = fmaf(l[t], alpha, rs);
+        // alpha is exactly 1 unless this row's max rose; past the first keys that is rare, so
+        // the accumulator rescale is skipped when no row of the wave needs it
+        if (__any(mnew != m[t])) {
+#pragma unroll
+          for (int dt = 0; dt < D / 32; dt++) acc[t][dt] *= alpha;
+        }
+        m[t] = mnew;
+      }
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        u16x8 vfr[D / 32];
+#pragma unroll
+        for (int dt = 0; dt < D / 32; dt++) {
+          const int d = dt * 32 + n;
+          vfr[dt] = *(const u16x8*)(Vt + d * CS + trot(d, sub * 32 + 16 * c + 8 * h));
+        }
+        u16x8 pb[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) pb[t] = pack8<T>(s[t], 8 * c);
+#pragma unroll
+        for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+          for (int t = 0; t < NT; t++) acc[t][dt] = T::mfma32(vfr[dt], pb[t], acc[t][dt]);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int row = wq0 + 32 * t + n;
+    const float total = l[t] + __shfl_xor(l[t], 32);
+    store_transposed<T, D>(out + b * (int64_t)t_q * D, acc[t], row, t_q, 1.f / total);
+    if (h == 0 && row < t_q) lse[b * (int64_t)t_q + row] = m[t] * scale + logf(total);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// dQ pass: resident query rows (NT tiles per wave), keys streaming 32 at a time.
+template <typename T, int D, int NT, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_q_mfma(const u16* __restrict__ q, const u16* __restrict__ k,
                                                               const u16* __restrict__ v, const u16* __restrict__ dout,
                                                               const float* __restrict__ lse,
                                                               const float* __restrict__ delta,
                                                               const u16* __restrict__ mask, u16* __restrict__ dq,
-                                                              int64_t batch, int64_t t_q, int64_t t_k, float scale) {
-  constexpr int RS = D + 8, CS = TILE + 8;
+                                                              int64_t batch, int t_q, int t_k, float scale) {
+  constexpr int RS = D + 8, CS = TILE + 8, ROWS = 128 * NT;
   __shared__ __attribute__((aligned(16))) u16 Ks[TILE * RS];
   __shared__ __attribute__((aligned(16))) u16 Vs[TILE * RS];
   __shared__ __attribute__((aligned(16))) u16 Kt[D * CS];
-  __shared__ float Mk[TILE];
+  __shared__ __attribute__((aligned(16))) float Mk[TILE];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, n = lane & 31;
-  const int64_t nqb = (t_q + BLOCK_ROWS - 1) / BLOCK_ROWS;
+  // the wave index in a scalar register: the per-wave tile bounds and causal tests below are then
+  // uniform branches instead of exec-masked ones
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
+  const int64_t nqb = (t_q + ROWS - 1) / ROWS;
   const int64_t b = blockIdx.x % batch;
   const int64_t qb = nqb - 1 - blockIdx.x / batch;
-  const int64_t q0 = qb * BLOCK_ROWS, wq0 = q0 + wave * 32, row = wq0 + n;
-  const u16* qbase = q + b * t_q * D;
-  const u16* obase = dout + b * t_q * D;
-  const u16* kbase = k + b * t_k * D;
-  const u16* vbase = v + b * t_k * D;
+  const int q0 = (int)qb * ROWS, wq0 = q0 + wave * 32 * NT;
+  const Rows qrows(q + b * (int64_t)t_q * D, t_q, D), orows(dout + b * (int64_t)t_q * D, t_q, D);
+  const Rows krows(k + b * (int64_t)t_k * D, t_k, D), vrows(v + b * (int64_t)t_k * D, t_k, D);
   const float c2 = scale * LOG2E;
 
-  u16x8 qf[D / 16], of[D / 16];
+  u16x8 qf[NT][D / 16], of[NT][D / 16];
+  f32x16 acc[NT][D / 32];
+  float L2[NT], Dr[NT];
 #pragma unroll
-  for (int ds = 0; ds < D / 16; ds++) {
-    qf[ds] = row < t_q ? *(const u16x8*)(qbase + row * D + ds * 16 + 8 * h) : zero8();
-    of[ds] = row < t_q ? *(const u16x8*)(obase + row * D + ds * 16 + 8 * h) : zero8();
+  for (int t = 0; t < NT; t++) {
+    const int row = wq0 + 32 * t + n;
+#pragma unroll
+    for (int ds = 0; ds < D / 16; ds++) {
+      qf[t][ds] = qrows.load8(row * D + ds * 16 + 8 * h);
+      of[t][ds] = orows.load8(row * D + ds * 16 + 8 * h);
+    }
+    L2[t] = row < t_q ? lse[b * (int64_t)t_q + row] * LOG2E : 0.f;
+    Dr[t] = row < t_q ? delta[b * (int64_t)t_q + row] : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++) acc[t][dt] = zero16();
   }
-  const float L2 = row < t_q ? lse[b * t_q + row] * LOG2E : 0.f;
-  const float Dr = row < t_q ? delta[b * t_q + row] : 0.f;
 
-  f32x16 acc[D / 32];
-#pragma unroll
-  for (int dt = 0; dt < D / 32; dt++) acc[dt] = zero16();
-
-  const int64_t kend = CAUSAL ? (q0 + BLOCK_ROWS < t_k ? q0 + BLOCK_ROWS : t_k) : t_k;
-  const int ntiles = (int)((kend + TILE - 1) / TILE);
+  const int kend = CAUSAL ? (q0 + ROWS < t_k ? q0 + ROWS : t_k) : t_k;
+  const int ntiles = (kend + TILE - 1) / TILE;
   Stage<D> st;
-  st.load(kbase, vbase, 0, t_k);
+  st.load(krows, vrows, 0);
   for (int it = 0; it < ntiles; it++) {
-    const int64_t k0 = (int64_t)it * TILE;
+    const int k0 = it * TILE;
     if (it > 0) __syncthreads();
     st.store(Ks, Kt, Vs, nullptr);
     if (MASK && threadIdx.x < TILE) {
-      const int64_t key = k0 + threadIdx.x;
-      Mk[threadIdx.x] = key < t_k ? T::unpack(mask[b * t_k + key]) : 0.f;
+      const int key = k0 + threadIdx.x;
+      Mk[threadIdx.x] = key < t_k ? T::unpack(mask[b * (int64_t)t_k + key]) : 0.f;
     }
     __syncthreads();
-    if (it + 1 < ntiles) st.load(kbase, vbase, k0 + TILE, t_k);
-    if (CAUSAL && k0 > wq0 + 31) continue;
-
-    f32x16 s[2], dp[2];
+    if (it + 1 < ntiles) st.load(krows, vrows, k0 + TILE);
 #pragma unroll
     for (int sub = 0; sub < 2; sub++) {
-      s[sub] = zero16();
-      dp[sub] = zero16();
+      const int s0 = k0 + sub * 32;
+      f32x16 s[NT], dp[NT];
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        s[t] = zero16();
+        dp[t] = zero16();
+      }
 #pragma unroll
       for (int ds = 0; ds < D / 16; ds++) {
         const u16x8 a = *(const u16x8*)(Ks + (sub * 32 + n) * RS + ds * 16 + 8 * h);
-        s[sub] = T::mfma32(a, qf[ds], s[sub]);
         const u16x8 e = *(const u16x8*)(Vs + (sub * 32 + n) * RS + ds * 16 + 8 * h);
-        dp[sub] = T::mfma32(e, of[ds], dp[sub]);
-      }
-    }
-    const bool edge = (k0 + TILE > t_k) || MASK || (CAUSAL && k0 + TILE - 1 > wq0);
 #pragma unroll
-    for (int sub = 0; sub < 2; sub++)
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        float p = fast_exp2(fmaf(s[sub][i], c2, -L2));
-        if (edge) {
-          const int r = sub * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-          const int64_t key = k0 + r;
-          const bool hide = key >= t_k || (CAUSAL && key > row) || (MASK && Mk[r] == 0.f);
-          if (hide) p = 0.f;
+        for (int t = 0; t < NT; t++) {
+          s[t] = T::mfma32(a, qf[t][ds], s[t]);
+          dp[t] = T::mfma32(e, of[t][ds], dp[t]);
         }
-        s[sub][i] = p * (dp[sub][i] - Dr) * scale;
       }
+      const bool edge = (s0 + 32 > t_k) || MASK || (CAUSAL && s0 + 31 > wq0);
+      f32x4 mk[4];
+      if (MASK) read_mask(Mk, sub, h, mk);
 #pragma unroll
-    for (int sub = 0; sub < 2; sub++)
+      for (int t = 0; t < NT; t++) {
+        const int row = wq0 + 32 * t + n;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          float p = fast_exp2(fmaf(s[t][i], c2, -L2[t]));
+          if (edge) p = hidden<CAUSAL, MASK>(k0, sub, i, h, t_k, row, mk) ? 0.f : p;
+          s[t][i] = p * (dp[t][i] - Dr[t]) * scale;
+        }
+      }
 #pragma unroll
       for (int c = 0; c < 2; c++) {
-        u16x8 g;
+        u16x8 g[NT];
 #pragma unroll
-        for (int j = 0; j < 8; j++) g[j] = T::pack(s[sub][8 * c + j]);
+        for (int t = 0; t < NT; t++) g[t] = pack8<T>(s[t], 8 * c);
 #pragma unroll
         for (int dt = 0; dt < D / 32; dt++) {
           const int d = dt * 32 + n;
           const u16x8 a = *(const u16x8*)(Kt + d * CS + trot(d, sub * 32 + 16 * c + 8 * h));
-          acc[dt] = T::mfma32(a, g, acc[dt]);
+#pragma unroll
+          for (int t = 0; t < NT; t++) acc[t][dt] = T::mfma32(a, g[t], acc[t][dt]);
         }
       }
+    }
   }
-  store_transposed<T, D>(dq + b * t_q * D, acc, row, t_q, 1.f);
+#pragma unroll
+  for (int t = 0; t < NT; t++) store_transposed<T, D>(dq + b * (int64_t)t_q * D, acc[t], wq0 + 32 * t + n, t_q, 1.f);
 }
 
 // ---------------------------------------------------------------------------------------------
-// dK/dV pass: resident key rows, queries streaming.
-template <typename T, int D, bool CAUSAL, bool MASK>
+// dK/dV pass: resident key rows (NT tiles per wave), queries streaming 32 at a time.
+template <typename T, int D, int NT, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_mfma(const u16* __restrict__ q, const u16* __restrict__ k,
                                                                const u16* __restrict__ v, const u16* __restrict__ dout,
                                                                const float* __restrict__ lse,
                                                                const float* __restrict__ delta,
                                                                const u16* __restrict__ mask, u16* __restrict__ dk,
-                                                               u16* __restrict__ dv, int64_t batch, int64_t t_q,
-                                                               int64_t t_k, float scale) {
-  constexpr int RS = D + 8, CS = TILE + 8;
+                                                               u16* __restrict__ dv, int64_t batch, int t_q,
+                                                               int t_k, float scale) {
+  constexpr int RS = D + 8, CS = TILE + 8, ROWS = 128 * NT;
   __shared__ __attribute__((aligned(16))) u16 Qs[TILE * RS];
   __shared__ __attribute__((aligned(16))) u16 Os[TILE * RS];
   __shared__ __attribute__((aligned(16))) u16 Qt[D * CS];
@@ -369,134 +426,170 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_mfma(const u16* __rest
   __shared__ __attribute__((aligned(16))) float Ls[TILE];
   __shared__ __attribute__((aligned(16))) float Ds[TILE];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, n = lane & 31;
+  // the wave index in a scalar register: the per-wave tile bounds and causal tests below are then
+  // uniform branches instead of exec-masked ones
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
   const int64_t b = blockIdx.x % batch;
   const int64_t kb = blockIdx.x / batch;  // causal: the first keys are seen by the most queries
-  const int64_t k0 = kb * BLOCK_ROWS, wk0 = k0 + wave * 32, key = wk0 + n;
-  const u16* qbase = q + b * t_q * D;
-  const u16* obase = dout + b * t_q * D;
-  const u16* kbase = k + b * t_k * D;
-  const u16* vbase = v + b * t_k * D;
+  const int k0 = (int)kb * ROWS, wk0 = k0 + wave * 32 * NT;
+  const Rows qrows(q + b * (int64_t)t_q * D, t_q, D), orows(dout + b * (int64_t)t_q * D, t_q, D);
+  const Rows krows(k + b * (int64_t)t_k * D, t_k, D), vrows(v + b * (int64_t)t_k * D, t_k, D);
   const float c2 = scale * LOG2E;
 
-  u16x8 kf[D / 16], vf[D / 16];
+  u16x8 kf[NT][D / 16], vf[NT][D / 16];
+  f32x16 gk[NT][D / 32], gv[NT][D / 32];
+  bool live[NT];
 #pragma unroll
-  for (int ds = 0; ds < D / 16; ds++) {
-    kf[ds] = key < t_k ? *(const u16x8*)(kbase + key * D + ds * 16 + 8 * h) : zero8();
-    vf[ds] = key < t_k ? *(const u16x8*)(vbase + key * D + ds * 16 + 8 * h) : zero8();
-  }
-  const bool live = key < t_k && (!MASK || T::unpack(mask[b * t_k + key]) != 0.f);
-
-  f32x16 gk[D / 32], gv[D / 32];
+  for (int t = 0; t < NT; t++) {
+    const int key = wk0 + 32 * t + n;
 #pragma unroll
-  for (int dt = 0; dt < D / 32; dt++) {
-    gk[dt] = zero16();
-    gv[dt] = zero16();
+    for (int ds = 0; ds < D / 16; ds++) {
+      kf[t][ds] = krows.load8(key * D + ds * 16 + 8 * h);
+      vf[t][ds] = vrows.load8(key * D + ds * 16 + 8 * h);
+    }
+    live[t] = key < t_k;
+    if (MASK) live[t] = live[t] & (T::unpack(mask[b * (int64_t)t_k + (key < t_k ? key : t_k - 1)]) != 0.f);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++) {
+      gk[t][dt] = zero16();
+      gv[t][dt] = zero16();
+    }
   }
 
-  const int64_t qstart = CAUSAL ? k0 : 0;  // a causal key is seen by queries at or after it
-  const int ntiles = qstart < t_q ? (int)((t_q - qstart + TILE - 1) / TILE) : 0;
+  const int qstart = CAUSAL ? k0 : 0;  // a causal key is seen by queries at or after it
+  const int ntiles = qstart < t_q ? (t_q - qstart + TILE - 1) / TILE : 0;
   Stage<D> st;
-  if (ntiles > 0) st.load(qbase, obase, qstart, t_q);
+  if (ntiles > 0) st.load(qrows, orows, qstart);
   for (int it = 0; it < ntiles; it++) {
-    const int64_t r0 = qstart + (int64_t)it * TILE;
+    const int r0 = qstart + it * TILE;
     if (it > 0) __syncthreads();
     st.store(Qs, Qt, Os, Ot);
     if (threadIdx.x < TILE) {
-      const int64_t qq = r0 + threadIdx.x;
-      Ls[threadIdx.x] = qq < t_q ? lse[b * t_q + qq] * LOG2E : 0.f;
-      Ds[threadIdx.x] = qq < t_q ? delta[b * t_q + qq] : 0.f;
+      const int qq = r0 + threadIdx.x;
+      Ls[threadIdx.x] = qq < t_q ? lse[b * (int64_t)t_q + qq] * LOG2E : 0.f;
+      Ds[threadIdx.x] = qq < t_q ? delta[b * (int64_t)t_q + qq] : 0.f;
     }
     __syncthreads();
-    if (it + 1 < ntiles) st.load(qbase, obase, r0 + TILE, t_q);
-    if (CAUSAL && r0 + TILE - 1 < wk0) continue;  // every query of this tile is left of this wave's keys
-
-    f32x16 s[2], dp[2];
+    if (it + 1 < ntiles) st.load(qrows, orows, r0 + TILE);
 #pragma unroll
     for (int sub = 0; sub < 2; sub++) {
-      s[sub] = zero16();
-      dp[sub] = zero16();
+      const int s0 = r0 + sub * 32;
+      f32x16 s[NT], dp[NT];
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        s[t] = zero16();
+        dp[t] = zero16();
+      }
 #pragma unroll
       for (int ds = 0; ds < D / 16; ds++) {
         const u16x8 a = *(const u16x8*)(Qs + (sub * 32 + n) * RS + ds * 16 + 8 * h);
-        s[sub] = T::mfma32(a, kf[ds], s[sub]);
         const u16x8 e = *(const u16x8*)(Os + (sub * 32 + n) * RS + ds * 16 + 8 * h);
-        dp[sub] = T::mfma32(e, vf[ds], dp[sub]);
-      }
-    }
-    const bool edge = (r0 + TILE > t_q) || MASK || (CAUSAL && r0 < wk0 + 31);
 #pragma unroll
-    for (int sub = 0; sub < 2; sub++)
+        for (int t = 0; t < NT; t++) {
+          s[t] = T::mfma32(a, kf[t][ds], s[t]);
+          dp[t] = T::mfma32(e, vf[t][ds], dp[t]);
+        }
+      }
+      const bool edge = (s0 + 32 > t_q) || MASK || (CAUSAL && s0 < wk0 + 32 * NT - 1);
 #pragma unroll
       for (int g = 0; g < 4; g++) {
         const int rb = sub * 32 + 8 * g + 4 * h;
         const f32x4 l4 = *(const f32x4*)(Ls + rb);
         const f32x4 d4 = *(const f32x4*)(Ds + rb);
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int i = 4 * g + e;
-          float p = fast_exp2(fmaf(s[sub][i], c2, -l4[e]));
-          if (edge) {
-            const int64_t qq = r0 + rb + e;
-            const bool hide = qq >= t_q || (CAUSAL && qq < key) || !live;
-            if (hide) p = 0.f;
+        for (int t = 0; t < NT; t++) {
+          const int key = wk0 + 32 * t + n;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int i = 4 * g + e;
+            float p = fast_exp2(fmaf(s[t][i], c2, -l4[e]));
+            if (edge) {
+              const int qq = r0 + rb + e;
+              bool hide = (qq >= t_q) | !live[t];
+              if (CAUSAL) hide |= qq < key;
+              p = hide ? 0.f : p;
+            }
+            s[t][i] = p;
+            dp[t][i] = p * (dp[t][i] - d4[e]) * scale;
           }
-          s[sub][i] = p;
-          dp[sub][i] = p * (dp[sub][i] - d4[e]) * scale;
         }
       }
 #pragma unroll
-    for (int sub = 0; sub < 2; sub++)
-#pragma unroll
       for (int c = 0; c < 2; c++) {
-        u16x8 pb, gb;
+        u16x8 pb[NT], gb[NT];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-          pb[j] = T::pack(s[sub][8 * c + j]);
-          gb[j] = T::pack(dp[sub][8 * c + j]);
+        for (int t = 0; t < NT; t++) {
+          pb[t] = pack8<T>(s[t], 8 * c);
+          gb[t] = pack8<T>(dp[t], 8 * c);
         }
 #pragma unroll
         for (int dt = 0; dt < D / 32; dt++) {
           const int d = dt * 32 + n, pos = trot(d, sub * 32 + 16 * c + 8 * h);
           const u16x8 a = *(const u16x8*)(Ot + d * CS + pos);
-          gv[dt] = T::mfma32(a, pb, gv[dt]);
           const u16x8 e = *(const u16x8*)(Qt + d * CS + pos);
-          gk[dt] = T::mfma32(e, gb, gk[dt]);
+#pragma unroll
+          for (int t = 0; t < NT; t++) {
+            gv[t][dt] = T::mfma32(a, pb[t], gv[t][dt]);
+            gk[t][dt] = T::mfma32(e, gb[t], gk[t][dt]);
+          }
         }
       }
+    }
   }
-  store_transposed<T, D>(dk + b * t_k * D, gk, key, t_k, 1.f);
-  store_transposed<T, D>(dv + b * t_k * D, gv, key, t_k, 1.f);
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int key = wk0 + 32 * t + n;
+    store_transposed<T, D>(dk + b * (int64_t)t_k * D, gk[t], key, t_k, 1.f);
+    store_transposed<T, D>(dv + b * (int64_t)t_k * D, gv[t], key, t_k, 1.f);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
 
-template <typename T, int D, bool CAUSAL, bool MASK>
-int launch(SdpaPass pass, const SdpaArgs& a) {
+// Resident 32-row tiles per wave for each pass and head dim: 2 (each LDS operand read feeds two
+// MFMAs) wherever the accumulators still fit the register file.
+template <int D>
+constexpr int tiles_per_wave(SdpaPass pass) {
+  if (pass == SDPA_FWD) return 1;  // two workgroups per CU hide its latency better than operand reuse
+  return (pass == SDPA_BWD_KV && D == 128) ? 1 : 2;
+}
+
+template <typename T, int D, int NT, bool CAUSAL, bool MASK, SdpaPass PASS>
+int launch_nt(const SdpaArgs& a) {
+  constexpr SdpaPass pass = PASS;
   const int64_t rows = pass == SDPA_BWD_KV ? a.t_k : a.t_q;
-  const int64_t blocks = a.batch * ((rows + BLOCK_ROWS - 1) / BLOCK_ROWS);
+  const int64_t per = 128 * NT;
+  const int64_t blocks = a.batch * ((rows + per - 1) / per);
   if (blocks > 0x7fffffff) return fail(LIMN_HIP_EUNSUPPORTED, "sdpa: %lld workgroups exceed one launch", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(THREADS);
   const float scale = (float)a.scale;
   const u16* mask = (const u16*)a.mask;
-  switch (pass) {
-    case SDPA_FWD:
-      hipLaunchKernelGGL((sdpa_fwd_mfma<T, D, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q,
-                         (const u16*)a.k, (const u16*)a.v, mask, (u16*)a.out0, (float*)a.out1, a.batch, a.t_q, a.t_k,
-                         scale);
-      break;
-    case SDPA_BWD_Q:
-      hipLaunchKernelGGL((sdpa_bwd_q_mfma<T, D, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q,
-                         (const u16*)a.k, (const u16*)a.v, (const u16*)a.dout, (const float*)a.lse,
-                         (const float*)a.delta, mask, (u16*)a.out0, a.batch, a.t_q, a.t_k, scale);
-      break;
-    case SDPA_BWD_KV:
-      hipLaunchKernelGGL((sdpa_bwd_kv_mfma<T, D, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q,
-                         (const u16*)a.k, (const u16*)a.v, (const u16*)a.dout, (const float*)a.lse,
-                         (const float*)a.delta, mask, (u16*)a.out0, (u16*)a.out1, a.batch, a.t_q, a.t_k, scale);
-      break;
+  if constexpr (PASS == SDPA_FWD) {
+    hipLaunchKernelGGL((sdpa_fwd_mfma<T, D, NT, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q,
+                       (const u16*)a.k, (const u16*)a.v, mask, (u16*)a.out0, (float*)a.out1, a.batch, (int)a.t_q, (int)a.t_k,
+                       scale);
+  } else if constexpr (PASS == SDPA_BWD_Q) {
+    hipLaunchKernelGGL((sdpa_bwd_q_mfma<T, D, NT, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q,
+                       (const u16*)a.k, (const u16*)a.v, (const u16*)a.dout, (const float*)a.lse, (const float*)a.delta,
+                       mask, (u16*)a.out0, a.batch, (int)a.t_q, (int)a.t_k, scale);
+  } else {
+    hipLaunchKernelGGL((sdpa_bwd_kv_mfma<T, D, NT, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q,
+                       (const u16*)a.k, (const u16*)a.v, (const u16*)a.dout, (const float*)a.lse, (const float*)a.delta,
+                       mask, (u16*)a.out0, (u16*)a.out1, a.batch, (int)a.t_q, (int)a.t_k, scale);
   }
   return check_hip(hipGetLastError(), "launching an sdpa kernel");
+}
+
+template <typename T, int D, bool CAUSAL, bool MASK>
+int launch(SdpaPass pass, const SdpaArgs& a) {
+  switch (pass) {
+    case SDPA_FWD:
+      return launch_nt<T, D, tiles_per_wave<D>(SDPA_FWD), CAUSAL, MASK, SDPA_FWD>(a);
+    case SDPA_BWD_Q:
+      return launch_nt<T, D, tiles_per_wave<D>(SDPA_BWD_Q), CAUSAL, MASK, SDPA_BWD_Q>(a);
+    default:
+      return launch_nt<T, D, tiles_per_wave<D>(SDPA_BWD_KV), CAUSAL, MASK, SDPA_BWD_KV>(a);
+  }
 }
 
 template <typename T, int D>
@@ -516,6 +609,12 @@ int launch_dim(SdpaPass pass, const SdpaArgs& a) {
 
 bool mfma_supports(int dtype, int64_t hd, int64_t hd_v) {
   return (dtype == LIMN_HIP_BFLOAT16 || dtype == LIMN_HIP_FLOAT16) && hd == hd_v && (hd == 64 || hd == 128);
+}
+
+bool mfma_fits(int64_t t_q, int64_t t_k, int64_t hd) {
+  // per-head offsets are 32-bit inside the kernels
+  const int64_t limit = ((int64_t)1 << 31) - 1;
+  return t_q * hd < limit && t_k * hd < limit;
 }
 
 int launch_sdpa_mfma(SdpaPass pass, const SdpaArgs& a) {
