@@ -32,13 +32,26 @@ import numpy as np
 
 MFMA_BF16_PEAK = 2.5e15  # dense bf16 MFMA flop/s, MI355X published
 HBM_PEAK = 8.0e12  # bytes/s
+TRAFFIC = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+
+
+def traffic(key: str):
+    """HBM bytes per launch of one kernel (read + written), from the rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes recorded in profiles/hbm_traffic.json, each counter scaled by what it reads
+    for a plain copy of known size. None when that kernel has no recorded pass."""
+    try:
+        with open(TRAFFIC) as f:
+            entry = json.load(f)["kernels"].get(key)
+    except (OSError, ValueError, KeyError):
+        return None
+    return None if entry is None else entry["traffic"]
 
 
 def parse() -> argparse.Namespace:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument(
         "--workload",
@@ -225,7 +238,7 @@ def bench_c2(dev, steps: int, warmup: int) -> dict:
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK, 4),
-            "traffic": None,
+            "traffic": traffic(f"c2:k{dom}"),
         },
     }
 
@@ -276,7 +289,7 @@ def bench_c3(dev, steps: int, warmup: int) -> dict:
             "peak": MFMA_BF16_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": round(flops / (mm * 1e-3) / MFMA_BF16_PEAK, 4),
-            "traffic": None,
+            "traffic": traffic("c3:matmul_mfma<BF16,256,256,true,false,0>"),
         },
     }
 
@@ -369,6 +382,12 @@ def main() -> int:
     step_flops = 7 * U
     kernel_flops = {"sdpa": 2 * U, "sdpa_bwd_q": 1 * U, "sdpa_bwd_kv": 4 * U}
     names = ["sdpa", "sdpa_bwd_q", "sdpa_bwd_kv"]
+    # the template instance each CUSTOM name runs at this configuration (rocprofv3's kernel names)
+    KERNEL_SYMBOL = {
+        "sdpa": "sdpa_fwd_mfma<BF16,128,1,true,false>",
+        "sdpa_bwd_q": "sdpa_bwd_q_mfma<BF16,128,2,true,false>",
+        "sdpa_bwd_kv": "sdpa_bwd_kv_mfma<BF16,128,1,true,false>",
+    }
     dom = int(np.argmax(per))
     achieved = kernel_flops[names[dom]] / (per[dom] * 1e-3)
     value = step_flops / (ms * 1e-3)
@@ -403,7 +422,7 @@ def main() -> int:
             "peak": MFMA_BF16_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_BF16_PEAK, 4),
-            "traffic": None,
+            "traffic": traffic(f"c4:{KERNEL_SYMBOL[names[dom]]}"),
         },
         "device": {"arch": dev.arch, "compute_units": dev.compute_units},
     }
