@@ -63,7 +63,10 @@ static int validate(SdpaPass pass, const SdpaArgs& a) {
 static int run(SdpaPass pass, const SdpaArgs& a) {
   const int rc = validate(pass, a);
   if (rc != LIMN_HIP_OK) return rc;
-  if (mfma_supports(a.dtype, a.hd, a.hd_v) && mfma_fits(a.t_q, a.t_k, a.hd)) return launch_sdpa_mfma(pass, a);
+  // the MFMA forward keeps each row's running max over raw scores, which orders the scaled scores
+  // only for a positive scale; the backward passes use the saved L and take any scale
+  const bool mfma_scale = pass != SDPA_FWD || a.scale > 0;
+  if (mfma_supports(a.dtype, a.hd, a.hd_v) && mfma_fits(a.t_q, a.t_k, a.hd) && mfma_scale) return launch_sdpa_mfma(pass, a);
   if (rows_supports(a.dtype, a.hd, a.hd_v)) return launch_sdpa_rows(pass, a);
   return fail(LIMN_HIP_EUNSUPPORTED, "%s: no kernel for head dims %lld and %lld (at most 256)", pass_name(pass),
               (long long)a.hd, (long long)a.hd_v);

@@ -17,7 +17,7 @@
 // so 16-byte reads across a 32-row operand are conflict-free), so each MFMA operand is one
 // ds_read_b128. An operand that is k-contiguous in memory is staged with 16-byte row loads;
 // one that is m- (or n-) contiguous is loaded 4 k-rows x 8 columns per thread and transposed
-// in registers on the way into LDS, its k positions rotated per 8-row group so that those
+// in registers on the way into LDS, its k positions rotated per 16-row group so that those
 // transposed writes spread over the banks.
 
 #include "matmul.h"
@@ -35,10 +35,26 @@ __device__ __forceinline__ u16x8 zero8() {
 }
 
 // k position of element k in LDS row `row` of an operand staged from row-contiguous memory:
-// rotated by 8 per 8-row group (identity for k-contiguous staging).
+// rotated by 8 per 16-row group (identity for k-contiguous staging). gfx950's LDS has 64
+// four-byte banks and serves 16 lanes of a 16-byte read (32 lanes of an 8-byte write) per cycle.
+// The row stride LS is 36 banks, so an operand read (16 consecutive rows, one rotation) starts
+// in 16 distinct 4-bank groups; a staging write (rows 8 apart) would land every even and every
+// odd row on one group, and the rotation by row >> 4 spreads them over all 16. Together with
+// the lane-to-block map of OperandStage (k groups of opposite parity, 8 bytes apart, in the
+// two 16-lane halves) the 32 lanes of a write fill all 64 banks.
 template <bool KCONTIG>
 __device__ __forceinline__ int kpos(int row, int k) {
-  return KCONTIG ? k : ((k + 8 * ((row >> 3) & 7)) & (BK - 1));
+  return KCONTIG ? k : ((k + 8 * ((row >> 4) & 7)) & (BK - 1));
+}
+
+// Block `blk` of a row-contiguous operand stage -> (8-row chunk rc, 4-deep k group kg): lanes
+// 0-15 take 16 consecutive row chunks with an even k group, lanes 16-31 the same chunks with the
+// next (odd) one; loads stay 256-byte coalesced per k row.
+template <int ROWS>
+__device__ __forceinline__ void stage_block(int blk, int& rc, int& kg) {
+  constexpr int R16 = ROWS / 128;  // 16-chunk groups of rows
+  rc = (blk & 15) | (((blk >> 5) % R16) << 4);
+  kg = ((blk >> 4) & 1) | (((blk >> 5) / R16) << 1);
 }
 
 // One operand's stage: ROWS (m or n) x BK values, staged into an LDS tile [row][k].
@@ -64,7 +80,8 @@ struct OperandStage {
 #pragma unroll
       for (int s = 0; s < LOADS / 4; s++) {
         const int blk = threadIdx.x + s * MM_THREADS;
-        const int rc = blk % (ROWS / 8), kg = blk / (ROWS / 8);
+        int rc, kg;
+        stage_block<ROWS>(blk, rc, kg);
         const int64_t gr = row0 + rc * 8;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
@@ -87,7 +104,8 @@ struct OperandStage {
 #pragma unroll
       for (int s = 0; s < LOADS / 4; s++) {
         const int blk = threadIdx.x + s * MM_THREADS;
-        const int rc = blk % (ROWS / 8), kg = blk / (ROWS / 8);
+        int rc, kg;
+        stage_block<ROWS>(blk, rc, kg);
 #pragma unroll
         for (int c = 0; c < 8; c++) {
           u16x4 t = {r[4 * s][c], r[4 * s + 1][c], r[4 * s + 2][c], r[4 * s + 3][c]};

@@ -36,6 +36,8 @@ constexpr int WAVES = 4;
 constexpr int THREADS = 64 * WAVES;
 constexpr int TILE = 64;
 constexpr float LOG2E = 1.4426950408889634f;
+// The forward lets probabilities reach 2^RESCALE_LOG2 before it moves a row's reference max.
+constexpr float RESCALE_LOG2 = 8.f;
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 
@@ -48,11 +50,20 @@ __device__ __forceinline__ int tpos(int r) {
   return (r & ~31) | (gp << 2) | (r & 3);
 }
 
-// A transposed tile's row `d` stores its TILE positions rotated by 8 * ((d >> 3) & 7): the
-// staging writes 8 rows apart then land in 8 different 16-byte bank groups, while an MFMA
-// operand read (8 consecutive positions starting at a multiple of 8, one row per lane)
-// stays one contiguous 16-byte word.
-__device__ __forceinline__ int trot(int d, int pos) { return (pos + 8 * ((d >> 3) & 7)) & (TILE - 1); }
+// A transposed tile's row `d` stores its TILE positions rotated by 8 * ((d >> 4) & 7).
+// gfx950's LDS has 64 four-byte banks and serves 16 lanes of a 16-byte access (32 lanes of an
+// 8-byte one) per cycle. The row stride of TILE + 8 elements is 36 banks, so the 16 consecutive
+// rows an MFMA operand read touches per cycle start in 16 distinct 4-bank groups as long as they
+// share a rotation, which rows 16-aligned do. A staging store (one 8-byte column piece per lane,
+// rows 8 apart) would put every even and every odd row chunk on the same bank group; the
+// rotation by row >> 4 spreads those 16 rows over the 16 groups, and `stage_group` gives the two
+// 16-lane halves of each 32 lanes the row groups whose positions are 8 bytes apart, so together
+// they fill all 64 banks.
+__device__ __forceinline__ int trot(int d, int pos) { return (pos + 8 * ((d >> 4) & 7)) & (TILE - 1); }
+
+// The 4-row group staged by the threads with group index j: bits 0 and 1 swapped, so lanes
+// 0-15 and 16-31 of a wave carry groups 4i and 4i + 2, which tpos() puts 8 bytes apart.
+__device__ __forceinline__ int stage_group(int j) { return (j & ~3) | ((j & 1) << 1) | ((j >> 1) & 1); }
 
 __device__ __forceinline__ u16x8 zero8() {
   u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -96,7 +107,7 @@ struct Stage {
       const int idx = threadIdx.x + s * THREADS;
       if (idx < 2 * PER_TILE) {
         const int which = idx / PER_TILE, w = idx - which * PER_TILE;
-        const int col = w % COLS, grp = w / COLS;
+        const int col = w % COLS, grp = stage_group(w / COLS);
         const Rows& m = which ? m1 : m0;
 #pragma unroll
         for (int e = 0; e < 4; e++) r[s][e] = m.load8((row0 + grp * 4 + e) * D + col * 8);
@@ -112,7 +123,7 @@ struct Stage {
       const int idx = threadIdx.x + s * THREADS;
       if (idx < 2 * PER_TILE) {
         const int which = idx / PER_TILE, w = idx - which * PER_TILE;
-        const int col = w % COLS, grp = w / COLS;
+        const int col = w % COLS, grp = stage_group(w / COLS);
         u16* rows = which ? rows1 : rows0;
         u16* cols = which ? cols1 : cols0;
         if (rows != nullptr) {
@@ -150,23 +161,35 @@ __device__ __forceinline__ void store_transposed(u16* base, const f32x16* acc, i
   }
 }
 
-// The streamed-key mask of one 32-key half, as item-ordered float4s: mk[g][e] belongs to key
-// offset sub * 32 + 8 * g + 4 * h + e, the key of accumulator item 4 * g + e.
-__device__ __forceinline__ void read_mask(const float* Mk, int sub, int h, f32x4 (&mk)[4]) {
-#pragma unroll
-  for (int g = 0; g < 4; g++) mk[g] = *(const f32x4*)(Mk + sub * 32 + 8 * g + 4 * h);
+// One batch row of the key mask, read through a buffer resource: entries past t_k read as zero,
+// which is "hidden", so the last tile needs no bounds test.
+struct MaskRow {
+  __amdgpu_buffer_rsrc_t rsrc;
+  __device__ __forceinline__ MaskRow(const u16* base, int t_k) {
+    rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, t_k * 2, 0x00020000);
+  }
+  __device__ __forceinline__ u16 load(int key) const { return __builtin_amdgcn_raw_buffer_load_b16(rsrc, key * 2, 0, 0); }
+};
+
+// The live keys of a 64-key tile as one wave-uniform 64-bit word (bit r = key k0 + r is visible):
+// each lane holds the mask entry of key k0 + lane, one 2-byte load per lane per tile, issued a
+// tile ahead. Nothing of the mask goes through LDS or holds vector registers across the tile.
+template <typename T>
+__device__ __forceinline__ uint64_t live_keys(u16 entry) {
+  return __ballot(T::unpack(entry) != 0.f);
 }
 
 // Whether accumulator item i of a 32-key half is a key that `row` may not see: past t_k, right of
-// the row under a causal mask, or zero in the key mask. Bitwise terms on values already in
-// registers, applied by the callers as selects: the short-circuit form, whose LDS read of the mask
-// sat under a branch, was compiled into code that left item 0 visible whatever its mask said.
+// the row under a causal mask, or zero in the key mask (`mb` = the tile's live-key word shifted
+// to the lane's first key, sub * 32 + 4 * h). Bitwise terms applied by the callers as selects: a
+// short-circuit form, whose mask read sat under a branch, was compiled into code that left item 0
+// visible whatever its mask said.
 template <bool CAUSAL, bool MASK>
-__device__ __forceinline__ bool hidden(int k0, int sub, int i, int h, int t_k, int row, const f32x4 (&mk)[4]) {
+__device__ __forceinline__ bool hidden(int k0, int sub, int i, int h, int t_k, int row, unsigned mb) {
   const int key = k0 + sub * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
   bool hide = key >= t_k;
   if (CAUSAL) hide |= key > row;
-  if (MASK) hide |= mk[i >> 2][i & 3] == 0.f;
+  if (MASK) hide |= ((mb >> (8 * (i >> 2) + (i & 3))) & 1u) == 0u;
   return hide;
 }
 
@@ -184,7 +207,6 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
   constexpr int RS = D + 8, CS = TILE + 8, ROWS = 128 * NT;
   __shared__ __attribute__((aligned(16))) u16 Ks[TILE * RS];
   __shared__ __attribute__((aligned(16))) u16 Vt[D * CS];
-  __shared__ __attribute__((aligned(16))) float Mk[TILE];
 
   // the wave index in a scalar register: the per-wave tile bounds and causal tests below are then
   // uniform branches instead of exec-masked ones
@@ -195,7 +217,7 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
   const int q0 = (int)qb * ROWS, wq0 = q0 + wave * 32 * NT;
   const Rows qrows(q + b * (int64_t)t_q * D, t_q, D);
   const Rows krows(k + b * (int64_t)t_k * D, t_k, D), vrows(v + b * (int64_t)t_k * D, t_k, D);
-  const float c2 = scale * LOG2E;
+  const float c2 = scale * LOG2E, lift = RESCALE_LOG2 / c2;  // scale > 0 (the C ABI routes others away)
 
   u16x8 qf[NT][D / 16];
   f32x16 acc[NT][D / 32];
@@ -215,16 +237,19 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
   const int ntiles = (kend + TILE - 1) / TILE;
   Stage<D> st;
   st.load(krows, vrows, 0);
+  const MaskRow mrow(MASK ? mask + b * (int64_t)t_k : nullptr, t_k);
+  u16 mnext = MASK ? mrow.load(lane) : (u16)0;
   for (int it = 0; it < ntiles; it++) {
     const int k0 = it * TILE;
     if (it > 0) __syncthreads();
     st.store(Ks, nullptr, nullptr, Vt);
-    if (MASK && threadIdx.x < TILE) {
-      const int key = k0 + threadIdx.x;
-      Mk[threadIdx.x] = key < t_k ? T::unpack(mask[b * (int64_t)t_k + key]) : 0.f;
-    }
     __syncthreads();
     if (it + 1 < ntiles) st.load(krows, vrows, k0 + TILE);
+    uint64_t live = ~0ull;
+    if (MASK) {
+      live = live_keys<T>(mnext);
+      if (it + 1 < ntiles) mnext = mrow.load(k0 + TILE + lane);
+    }
 #pragma unroll
     for (int sub = 0; sub < 2; sub++) {
       const int s0 = k0 + sub * 32;
@@ -239,24 +264,37 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
       for (int ds = 0; ds < D / 16; ds++)
 #pragma unroll
         for (int t = 0; t < NT; t++) s[t] = T::mfma32(kfr[ds], qf[t][ds], s[t]);
-      const bool edge = (s0 + 32 > t_k) || MASK || (CAUSAL && s0 + 31 > wq0);
-      f32x4 mk[4];
-      if (MASK) read_mask(Mk, sub, h, mk);
+      // a half needs masking when it runs past t_k, holds a hidden key, or crosses the diagonal
+      const unsigned half_live = (unsigned)(live >> (sub * 32));
+      const bool edge = (s0 + 32 > t_k) || (MASK && half_live != ~0u) || (CAUSAL && s0 + 31 > wq0);
+      const unsigned mb = (unsigned)(live >> (sub * 32 + 4 * h));
 #pragma unroll
       for (int t = 0; t < NT; t++) {
         const int row = wq0 + 32 * t + n;
         if (edge) {
 #pragma unroll
           for (int i = 0; i < 16; i++)
-            s[t][i] = hidden<CAUSAL, MASK>(k0, sub, i, h, t_k, row, mk) ? neg_inf() : s[t][i];
+            s[t][i] = hidden<CAUSAL, MASK>(k0, sub, i, h, t_k, row, mb) ? neg_inf() : s[t][i];
         }
         float mx = neg_inf();
 #pragma unroll
         for (int i = 0; i < 16; i++) mx = fmaxf(mx, s[t][i]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mnew = fmaxf(m[t], mx);
-        const float base = mnew == neg_inf() ? 0.f : mnew * c2;
-        const float alpha = fast_exp2(m[t] * c2 - base);
+        // m is the reference point of the row's exponentials, not its exact running max: it moves
+        // (and the totals are rescaled) only when a half's max passes it by more than `lift`, i.e.
+        // when some p would exceed 2^RESCALE_LOG2. Larger p are carried by the float totals and
+        // the 16-bit P operands as exactly as p <= 1, and the D/2 multiplies per lane of the
+        // rescale then run on the few halves whose max jumps, not on every half where some row's
+        // max creeps up.
+        if (__any(mx > m[t] + lift)) {
+          const float mnew = fmaxf(m[t], mx);
+          const float alpha = mnew == neg_inf() ? 1.f : fast_exp2((m[t] - mnew) * c2);
+          l[t] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < D / 32; dt++) acc[t][dt] *= alpha;
+          m[t] = mnew;
+        }
+        const float base = m[t] == neg_inf() ? 0.f : m[t] * c2;
         float rs = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
@@ -264,14 +302,7 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
           s[t][i] = p;
           rs += p;
         }
-        l[t] = fmaf(l[t], alpha, rs);
-        // alpha is exactly 1 unless this row's max rose; past the first keys that is rare, so
-        // the accumulator rescale is skipped when no row of the wave needs it
-        if (__any(mnew != m[t])) {
-#pragma unroll
-          for (int dt = 0; dt < D / 32; dt++) acc[t][dt] *= alpha;
-        }
-        m[t] = mnew;
+        l[t] += rs;
       }
 #pragma unroll
       for (int c = 0; c < 2; c++) {
@@ -313,7 +344,6 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_q_mfma(const u16* __restr
   __shared__ __attribute__((aligned(16))) u16 Ks[TILE * RS];
   __shared__ __attribute__((aligned(16))) u16 Vs[TILE * RS];
   __shared__ __attribute__((aligned(16))) u16 Kt[D * CS];
-  __shared__ __attribute__((aligned(16))) float Mk[TILE];
 
   // the wave index in a scalar register: the per-wave tile bounds and causal tests below are then
   // uniform branches instead of exec-masked ones
@@ -347,16 +377,19 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_q_mfma(const u16* __restr
   const int ntiles = (kend + TILE - 1) / TILE;
   Stage<D> st;
   st.load(krows, vrows, 0);
+  const MaskRow mrow(MASK ? mask + b * (int64_t)t_k : nullptr, t_k);
+  u16 mnext = MASK ? mrow.load(lane) : (u16)0;
   for (int it = 0; it < ntiles; it++) {
     const int k0 = it * TILE;
     if (it > 0) __syncthreads();
     st.store(Ks, Kt, Vs, nullptr);
-    if (MASK && threadIdx.x < TILE) {
-      const int key = k0 + threadIdx.x;
-      Mk[threadIdx.x] = key < t_k ? T::unpack(mask[b * (int64_t)t_k + key]) : 0.f;
-    }
     __syncthreads();
     if (it + 1 < ntiles) st.load(krows, vrows, k0 + TILE);
+    uint64_t live = ~0ull;
+    if (MASK) {
+      live = live_keys<T>(mnext);
+      if (it + 1 < ntiles) mnext = mrow.load(k0 + TILE + lane);
+    }
 #pragma unroll
     for (int sub = 0; sub < 2; sub++) {
       const int s0 = k0 + sub * 32;
@@ -376,16 +409,17 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_q_mfma(const u16* __restr
           dp[t] = T::mfma32(e, of[t][ds], dp[t]);
         }
       }
-      const bool edge = (s0 + 32 > t_k) || MASK || (CAUSAL && s0 + 31 > wq0);
-      f32x4 mk[4];
-      if (MASK) read_mask(Mk, sub, h, mk);
+      // a half needs masking when it runs past t_k, holds a hidden key, or crosses the diagonal
+      const unsigned half_live = (unsigned)(live >> (sub * 32));
+      const bool edge = (s0 + 32 > t_k) || (MASK && half_live != ~0u) || (CAUSAL && s0 + 31 > wq0);
+      const unsigned mb = (unsigned)(live >> (sub * 32 + 4 * h));
 #pragma unroll
       for (int t = 0; t < NT; t++) {
         const int row = wq0 + 32 * t + n;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
           float p = fast_exp2(fmaf(s[t][i], c2, -L2[t]));
-          if (edge) p = hidden<CAUSAL, MASK>(k0, sub, i, h, t_k, row, mk) ? 0.f : p;
+          if (edge) p = hidden<CAUSAL, MASK>(k0, sub, i, h, t_k, row, mb) ? 0.f : p;
           s[t][i] = p * (dp[t][i] - Dr[t]) * scale;
         }
       }
