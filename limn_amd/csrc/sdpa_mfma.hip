@@ -21,8 +21,12 @@
 // exchange with lane ^ 32 per tile), and a probability tile converted to bf16 *is* the
 // B operand of the next product without moving between lanes: the accumulator items 8c..8c+7
 // of a lane cover 8 of the 16 streamed rows of k-chunk c. The A operand of that product
-// reads the streamed operand transposed; it is staged into LDS transposed with its rows
-// permuted (tpos) so that those same 8 rows sit in one 16-byte LDS word.
+// is the streamed operand transposed: it is read from the same row-major LDS tile with gfx950's
+// transposing LDS read (ds_read_b64_tr_b16), addressed so that lane l gets exactly those 8 rows.
+//
+// LDS: each streamed tile is stored once, row-major with padded, permuted rows (tile_row), and
+// double-buffered: the next tile is written into the other buffer as soon as a wave finishes the
+// current one, behind one barrier per tile.
 //
 // 32x32 accumulator layout (CDNA3/CDNA4 matrix cores): lane l, item i holds
 // row 8*(i/4) + 4*(l/32) + i%4, column l%32.
@@ -41,29 +45,60 @@ constexpr float RESCALE_LOG2 = 8.f;
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 
-// Position of streamed row r (0..TILE-1) in a transposed LDS tile: within each 32-row
-// sub-tile the 4-row groups g = 4c + 2q + h are reordered to 4c + 2h + q, so the 8 rows
-// {16c + 8q + 4h + e} that lane half h feeds to k-chunk c are contiguous at 16c + 8h.
-__device__ __forceinline__ int tpos(int r) {
-  const int g = (r >> 2) & 7;
-  const int gp = (g & 4) | ((g & 1) << 1) | ((g >> 1) & 1);
-  return (r & ~31) | (gp << 2) | (r & 3);
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+// ---- LDS tiles -------------------------------------------------------------------------------
+// A streamed tile is TILE rows x D elements, rows padded to D + 8 elements (a 16-byte chunk more
+// than a multiple of 256 bytes, so consecutive physical rows start one 16-byte bank group apart),
+// with the streamed rows permuted: row 4q + j of each 32 is stored at physical row
+// (q >> 1) + 4j + 16 parity(q). gfx950's LDS has 64 banks of 4 bytes; measured on the MI355X, a
+// 16-byte read is served 16 lanes per cycle, the lanes of each 32-lane half grouped by the parity
+// of their quad index (lane >> 2) & 7; a transposing 8-byte read 32 lanes per cycle; a 16-byte
+// write 8 consecutive lanes per cycle. Against that the layout makes every access conflict-free:
+//   row operand reads (the 16 rows of one parity group, one chunk): the two quads q of a group
+//     with equal q >> 1 sit 16 physical rows apart, so the 16 rows start in 16 different groups;
+//   transposing reads (the 4 rows of an aligned quad, 4 chunks each): 4 physical rows apart, so
+//     their 64-byte windows tile the 256-byte bank line;
+//   staging writes (8 chunks of one row): contiguous.
+// Every address is a per-lane base plus a compile-time offset, so reads cost no address VALU.
+template <int D>
+constexpr int tile_stride() { return D + 8; }
+
+__device__ __forceinline__ int tile_row(int r) {
+  const int q = (r >> 2) & 7;
+  const int odd = (q ^ (q >> 1) ^ (q >> 2)) & 1;
+  return (r & ~31) | ((q >> 1) + 4 * (r & 3) + 16 * odd);
 }
 
-// A transposed tile's row `d` stores its TILE positions rotated by 8 * ((d >> 4) & 7).
-// gfx950's LDS has 64 four-byte banks and serves 16 lanes of a 16-byte access (32 lanes of an
-// 8-byte one) per cycle. The row stride of TILE + 8 elements is 36 banks, so the 16 consecutive
-// rows an MFMA operand read touches per cycle start in 16 distinct 4-bank groups as long as they
-// share a rotation, which rows 16-aligned do. A staging store (one 8-byte column piece per lane,
-// rows 8 apart) would put every even and every odd row chunk on the same bank group; the
-// rotation by row >> 4 spreads those 16 rows over the 16 groups, and `stage_group` gives the two
-// 16-lane halves of each 32 lanes the row groups whose positions are 8 bytes apart, so together
-// they fill all 64 banks.
-__device__ __forceinline__ int trot(int d, int pos) { return (pos + 8 * ((d >> 4) & 7)) & (TILE - 1); }
+// Element offset of element d of streamed row r.
+template <int D>
+__device__ __forceinline__ int tile_at(int r, int d) {
+  return tile_row(r) * tile_stride<D>() + d;
+}
 
-// The 4-row group staged by the threads with group index j: bits 0 and 1 swapped, so lanes
-// 0-15 and 16-31 of a wave carry groups 4i and 4i + 2, which tpos() puts 8 bytes apart.
-__device__ __forceinline__ int stage_group(int j) { return (j & ~3) | ((j & 1) << 1) | ((j >> 1) & 1); }
+// Row operand: elements 8c .. 8c + 7 of streamed row r, one ds_read_b128.
+template <int D>
+__device__ __forceinline__ u16x8 read_row(const u16* tile, int r, int c) {
+  return *(const u16x8*)(tile + tile_at<D>(r, 8 * c));
+}
+
+// Transposed operand: lane l gets X[k0 + 4 (l / 32) + 8 (j / 4) + j % 4][d0 + l % 32], j = 0..7,
+// of the tile X: the 8 streamed rows that items 8c..8c+7 of a lane's accumulator cover when
+// k0 = 16c, which is what pack8 turns into the B operand. Two ds_read_b64_tr_b16 (j / 4 = 0, 1):
+// within each 16-lane group, lane i receives item j' from the 8 bytes addressed by lane
+// 4 j' + i / 4, element i % 4; so lane r of the group addresses row k0 + 4 (l / 32) + 8 (j / 4) +
+// r / 4, columns d0 + 16 ((l / 16) % 2) + 4 (r % 4) .. + 3.
+template <int D>
+__device__ __forceinline__ u16x8 read_transposed(const u16* tile, int k0, int d0) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, i = lane & 15;
+  const int d = d0 + 16 * (g & 1) + 4 * (i & 3);
+  const int r = k0 + 4 * (g >> 1) + (i >> 2);
+  u16* base = (u16*)tile;
+  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(base + tile_at<D>(r, d)));
+  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(base + tile_at<D>(r + 8, d)));
+  return __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
 
 __device__ __forceinline__ u16x8 zero8() {
   u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -90,14 +125,14 @@ struct Rows {
   }
 };
 
-// Global -> registers -> LDS staging of one or two TILE x D row-major tiles. Each participating
-// thread carries a 4-row x 8-column block, so it can write its rows (16 B per row) into a
-// row-major LDS tile and its columns (8 B per column, 4 rows) into a transposed one.
+// Global -> registers -> LDS staging of two TILE x D row-major tiles. Each participating thread
+// carries one 16-byte column chunk of 4 consecutive rows; 8 consecutive lanes write 8 chunks of
+// one row.
 template <int D>
 struct Stage {
-  static constexpr int COLS = D / 8;           // 16-byte column chunks per row
-  static constexpr int PER_TILE = COLS * (TILE / 4);
-  static constexpr int SLOTS = (2 * PER_TILE + THREADS - 1) / THREADS;  // both tiles
+  static constexpr int COLS = D / 8;                  // 16-byte chunks per row
+  static constexpr int PER_TILE = COLS * (TILE / 4);  // (chunk, 4-row group) blocks per tile
+  static constexpr int SLOTS = (2 * PER_TILE + THREADS - 1) / THREADS;
   u16x8 r[SLOTS][4];
 
   // rows [row0, row0 + TILE) of both matrices; rows past their end read as zeros
@@ -107,7 +142,7 @@ struct Stage {
       const int idx = threadIdx.x + s * THREADS;
       if (idx < 2 * PER_TILE) {
         const int which = idx / PER_TILE, w = idx - which * PER_TILE;
-        const int col = w % COLS, grp = stage_group(w / COLS);
+        const int col = w % COLS, grp = w / COLS;
         const Rows& m = which ? m1 : m0;
 #pragma unroll
         for (int e = 0; e < 4; e++) r[s][e] = m.load8((row0 + grp * 4 + e) * D + col * 8);
@@ -115,30 +150,16 @@ struct Stage {
     }
   }
 
-  // rows0/cols0 receive tile 0, rows1/cols1 tile 1; a null destination is skipped.
-  __device__ __forceinline__ void store(u16* rows0, u16* cols0, u16* rows1, u16* cols1) {
-    constexpr int RS = D + 8, CS = TILE + 8;
+  __device__ __forceinline__ void store(u16* tile0, u16* tile1) {
 #pragma unroll
     for (int s = 0; s < SLOTS; s++) {
       const int idx = threadIdx.x + s * THREADS;
       if (idx < 2 * PER_TILE) {
         const int which = idx / PER_TILE, w = idx - which * PER_TILE;
-        const int col = w % COLS, grp = stage_group(w / COLS);
-        u16* rows = which ? rows1 : rows0;
-        u16* cols = which ? cols1 : cols0;
-        if (rows != nullptr) {
+        const int col = w % COLS, grp = w / COLS;
+        u16* tile = which ? tile1 : tile0;
 #pragma unroll
-          for (int e = 0; e < 4; e++) *(u16x8*)(rows + (grp * 4 + e) * RS + col * 8) = r[s][e];
-        }
-        if (cols != nullptr) {
-          const int p = tpos(grp * 4);
-#pragma unroll
-          for (int c = 0; c < 8; c++) {
-            u16x4 t = {r[s][0][c], r[s][1][c], r[s][2][c], r[s][3][c]};
-            const int d = col * 8 + c;
-            *(u16x4*)(cols + d * CS + trot(d, p)) = t;
-          }
-        }
+        for (int e = 0; e < 4; e++) *(u16x8*)(tile + tile_at<D>(grp * 4 + e, col * 8)) = r[s][e];
       }
     }
   }
@@ -204,9 +225,9 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
                                                             const u16* __restrict__ v, const u16* __restrict__ mask,
                                                             u16* __restrict__ out, float* __restrict__ lse, int64_t batch,
                                                             int t_q, int t_k, float scale) {
-  constexpr int RS = D + 8, CS = TILE + 8, ROWS = 128 * NT;
-  __shared__ __attribute__((aligned(16))) u16 Ks[TILE * RS];
-  __shared__ __attribute__((aligned(16))) u16 Vt[D * CS];
+  constexpr int ROWS = 128 * NT;
+  __shared__ __attribute__((aligned(16))) u16 Ks[2][TILE * tile_stride<D>()];
+  __shared__ __attribute__((aligned(16))) u16 Vs[2][TILE * tile_stride<D>()];
 
   // the wave index in a scalar register: the per-wave tile bounds and causal tests below are then
   // uniform branches instead of exec-masked ones
@@ -237,14 +258,15 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
   const int ntiles = (kend + TILE - 1) / TILE;
   Stage<D> st;
   st.load(krows, vrows, 0);
+  st.store(Ks[0], Vs[0]);
+  if (ntiles > 1) st.load(krows, vrows, TILE);
   const MaskRow mrow(MASK ? mask + b * (int64_t)t_k : nullptr, t_k);
   u16 mnext = MASK ? mrow.load(lane) : (u16)0;
+  __syncthreads();
   for (int it = 0; it < ntiles; it++) {
-    const int k0 = it * TILE;
-    if (it > 0) __syncthreads();
-    st.store(Ks, nullptr, nullptr, Vt);
-    __syncthreads();
-    if (it + 1 < ntiles) st.load(krows, vrows, k0 + TILE);
+    const int k0 = it * TILE, buf = it & 1;
+    const u16* Kt = Ks[buf];
+    const u16* Vt = Vs[buf];
     uint64_t live = ~0ull;
     if (MASK) {
       live = live_keys<T>(mnext);
@@ -256,7 +278,7 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
       // every K fragment of this half first, then the MFMA chain: the reads overlap each other
       u16x8 kfr[D / 16];
 #pragma unroll
-      for (int ds = 0; ds < D / 16; ds++) kfr[ds] = *(const u16x8*)(Ks + (sub * 32 + n) * RS + ds * 16 + 8 * h);
+      for (int ds = 0; ds < D / 16; ds++) kfr[ds] = read_row<D>(Kt, sub * 32 + n, 2 * ds + h);
       f32x16 s[NT];
 #pragma unroll
       for (int t = 0; t < NT; t++) s[t] = zero16();
@@ -308,10 +330,7 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
       for (int c = 0; c < 2; c++) {
         u16x8 vfr[D / 32];
 #pragma unroll
-        for (int dt = 0; dt < D / 32; dt++) {
-          const int d = dt * 32 + n;
-          vfr[dt] = *(const u16x8*)(Vt + d * CS + trot(d, sub * 32 + 16 * c + 8 * h));
-        }
+        for (int dt = 0; dt < D / 32; dt++) vfr[dt] = read_transposed<D>(Vt, sub * 32 + 16 * c, dt * 32);
         u16x8 pb[NT];
 #pragma unroll
         for (int t = 0; t < NT; t++) pb[t] = pack8<T>(s[t], 8 * c);
@@ -321,6 +340,12 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
           for (int t = 0; t < NT; t++) acc[t][dt] = T::mfma32(vfr[dt], pb[t], acc[t][dt]);
       }
     }
+    // the next tile into the other buffer (free since the last barrier), then the load after it
+    if (it + 1 < ntiles) {
+      st.store(Ks[buf ^ 1], Vs[buf ^ 1]);
+      if (it + 2 < ntiles) st.load(krows, vrows, k0 + 2 * TILE);
+    }
+    __syncthreads();
   }
 #pragma unroll
   for (int t = 0; t < NT; t++) {
@@ -334,16 +359,15 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
 // ---------------------------------------------------------------------------------------------
 // dQ pass: resident query rows (NT tiles per wave), keys streaming 32 at a time.
 template <typename T, int D, int NT, bool CAUSAL, bool MASK>
-__global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_q_mfma(const u16* __restrict__ q, const u16* __restrict__ k,
+__global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_bwd_q_mfma(const u16* __restrict__ q, const u16* __restrict__ k,
                                                               const u16* __restrict__ v, const u16* __restrict__ dout,
                                                               const float* __restrict__ lse,
                                                               const float* __restrict__ delta,
                                                               const u16* __restrict__ mask, u16* __restrict__ dq,
                                                               int64_t batch, int t_q, int t_k, float scale) {
-  constexpr int RS = D + 8, CS = TILE + 8, ROWS = 128 * NT;
-  __shared__ __attribute__((aligned(16))) u16 Ks[TILE * RS];
-  __shared__ __attribute__((aligned(16))) u16 Vs[TILE * RS];
-  __shared__ __attribute__((aligned(16))) u16 Kt[D * CS];
+  constexpr int ROWS = 128 * NT;
+  __shared__ __attribute__((aligned(16))) u16 Ks[2][TILE * tile_stride<D>()];
+  __shared__ __attribute__((aligned(16))) u16 Vs[2][TILE * tile_stride<D>()];
 
   // the wave index in a scalar register: the per-wave tile bounds and causal tests below are then
   // uniform branches instead of exec-masked ones
@@ -368,7 +392,7 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_q_mfma(const u16* __restr
       of[t][ds] = orows.load8(row * D + ds * 16 + 8 * h);
     }
     L2[t] = row < t_q ? lse[b * (int64_t)t_q + row] * LOG2E : 0.f;
-    Dr[t] = row < t_q ? delta[b * (int64_t)t_q + row] : 0.f;
+    Dr[t] = row < t_q ? delta[b * (int64_t)t_q + row] * scale : 0.f;  // ds = p (dp scale - delta scale)
 #pragma unroll
     for (int dt = 0; dt < D / 32; dt++) acc[t][dt] = zero16();
   }
@@ -377,14 +401,15 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_q_mfma(const u16* __restr
   const int ntiles = (kend + TILE - 1) / TILE;
   Stage<D> st;
   st.load(krows, vrows, 0);
+  st.store(Ks[0], Vs[0]);
+  if (ntiles > 1) st.load(krows, vrows, TILE);
   const MaskRow mrow(MASK ? mask + b * (int64_t)t_k : nullptr, t_k);
   u16 mnext = MASK ? mrow.load(lane) : (u16)0;
+  __syncthreads();
   for (int it = 0; it < ntiles; it++) {
-    const int k0 = it * TILE;
-    if (it > 0) __syncthreads();
-    st.store(Ks, Kt, Vs, nullptr);
-    __syncthreads();
-    if (it + 1 < ntiles) st.load(krows, vrows, k0 + TILE);
+    const int k0 = it * TILE, buf = it & 1;
+    const u16* Kb = Ks[buf];
+    const u16* Vb = Vs[buf];
     uint64_t live = ~0ull;
     if (MASK) {
       live = live_keys<T>(mnext);
@@ -401,8 +426,8 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_q_mfma(const u16* __restr
       }
 #pragma unroll
       for (int ds = 0; ds < D / 16; ds++) {
-        const u16x8 a = *(const u16x8*)(Ks + (sub * 32 + n) * RS + ds * 16 + 8 * h);
-        const u16x8 e = *(const u16x8*)(Vs + (sub * 32 + n) * RS + ds * 16 + 8 * h);
+        const u16x8 a = read_row<D>(Kb, sub * 32 + n, 2 * ds + h);
+        const u16x8 e = read_row<D>(Vb, sub * 32 + n, 2 * ds + h);
 #pragma unroll
         for (int t = 0; t < NT; t++) {
           s[t] = T::mfma32(a, qf[t][ds], s[t]);
@@ -413,16 +438,22 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_q_mfma(const u16* __restr
       const unsigned half_live = (unsigned)(live >> (sub * 32));
       const bool edge = (s0 + 32 > t_k) || (MASK && half_live != ~0u) || (CAUSAL && s0 + 31 > wq0);
       const unsigned mb = (unsigned)(live >> (sub * 32 + 4 * h));
+      // probabilities, then the masking as one uniform block of selects (a test per item would be
+      // compiled into a branch per item), then dS
 #pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const int row = wq0 + 32 * t + n;
+      for (int t = 0; t < NT; t++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-          float p = fast_exp2(fmaf(s[t][i], c2, -L2[t]));
-          if (edge) p = hidden<CAUSAL, MASK>(k0, sub, i, h, t_k, row, mb) ? 0.f : p;
-          s[t][i] = p * (dp[t][i] - Dr[t]) * scale;
-        }
+        for (int i = 0; i < 16; i++) s[t][i] = fast_exp2(fmaf(s[t][i], c2, -L2[t]));
+      if (edge) {
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+          for (int i = 0; i < 16; i++) s[t][i] = hidden<CAUSAL, MASK>(k0, sub, i, h, t_k, wq0 + 32 * t + n, mb) ? 0.f : s[t][i];
       }
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) s[t][i] *= fmaf(dp[t][i], scale, -Dr[t]);
 #pragma unroll
       for (int c = 0; c < 2; c++) {
         u16x8 g[NT];
@@ -430,13 +461,17 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_q_mfma(const u16* __restr
         for (int t = 0; t < NT; t++) g[t] = pack8<T>(s[t], 8 * c);
 #pragma unroll
         for (int dt = 0; dt < D / 32; dt++) {
-          const int d = dt * 32 + n;
-          const u16x8 a = *(const u16x8*)(Kt + d * CS + trot(d, sub * 32 + 16 * c + 8 * h));
+          const u16x8 a = read_transposed<D>(Kb, sub * 32 + 16 * c, dt * 32);
 #pragma unroll
           for (int t = 0; t < NT; t++) acc[t][dt] = T::mfma32(a, g[t], acc[t][dt]);
         }
       }
     }
+    if (it + 1 < ntiles) {
+      st.store(Ks[buf ^ 1], Vs[buf ^ 1]);
+      if (it + 2 < ntiles) st.load(krows, vrows, k0 + 2 * TILE);
+    }
+    __syncthreads();
   }
 #pragma unroll
   for (int t = 0; t < NT; t++) store_transposed<T, D>(dq + b * (int64_t)t_q * D, acc[t], wq0 + 32 * t + n, t_q, 1.f);
@@ -452,13 +487,11 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_mfma(const u16* __rest
                                                                const u16* __restrict__ mask, u16* __restrict__ dk,
                                                                u16* __restrict__ dv, int64_t batch, int t_q,
                                                                int t_k, float scale) {
-  constexpr int RS = D + 8, CS = TILE + 8, ROWS = 128 * NT;
-  __shared__ __attribute__((aligned(16))) u16 Qs[TILE * RS];
-  __shared__ __attribute__((aligned(16))) u16 Os[TILE * RS];
-  __shared__ __attribute__((aligned(16))) u16 Qt[D * CS];
-  __shared__ __attribute__((aligned(16))) u16 Ot[D * CS];
-  __shared__ __attribute__((aligned(16))) float Ls[TILE];
-  __shared__ __attribute__((aligned(16))) float Ds[TILE];
+  constexpr int ROWS = 128 * NT;
+  __shared__ __attribute__((aligned(16))) u16 Qs[2][TILE * tile_stride<D>()];
+  __shared__ __attribute__((aligned(16))) u16 Os[2][TILE * tile_stride<D>()];
+  __shared__ __attribute__((aligned(16))) float Ls[2][TILE];  // lse * log2(e) of the tile's queries
+  __shared__ __attribute__((aligned(16))) float Ds[2][TILE];  // delta * scale
 
   // the wave index in a scalar register: the per-wave tile bounds and causal tests below are then
   // uniform branches instead of exec-masked ones
@@ -492,19 +525,35 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_mfma(const u16* __rest
 
   const int qstart = CAUSAL ? k0 : 0;  // a causal key is seen by queries at or after it
   const int ntiles = qstart < t_q ? (t_q - qstart + TILE - 1) / TILE : 0;
+  // the per-query statistics of a tile travel like its rows: loaded a tile ahead into registers
+  // of the first wave, written into the tile's buffer with them
+  auto stats_load = [&](int r0, float& ls, float& dl) {
+    const int qq = r0 + (int)threadIdx.x;
+    ls = qq < t_q ? lse[b * (int64_t)t_q + qq] * LOG2E : 0.f;
+    dl = qq < t_q ? delta[b * (int64_t)t_q + qq] * scale : 0.f;
+  };
   Stage<D> st;
-  if (ntiles > 0) st.load(qrows, orows, qstart);
-  for (int it = 0; it < ntiles; it++) {
-    const int r0 = qstart + it * TILE;
-    if (it > 0) __syncthreads();
-    st.store(Qs, Qt, Os, Ot);
+  float lnext = 0.f, dnext = 0.f;
+  if (ntiles > 0) {
+    st.load(qrows, orows, qstart);
+    if (threadIdx.x < TILE) stats_load(qstart, lnext, dnext);
+    st.store(Qs[0], Os[0]);
     if (threadIdx.x < TILE) {
-      const int qq = r0 + threadIdx.x;
-      Ls[threadIdx.x] = qq < t_q ? lse[b * (int64_t)t_q + qq] * LOG2E : 0.f;
-      Ds[threadIdx.x] = qq < t_q ? delta[b * (int64_t)t_q + qq] : 0.f;
+      Ls[0][threadIdx.x] = lnext;
+      Ds[0][threadIdx.x] = dnext;
     }
-    __syncthreads();
-    if (it + 1 < ntiles) st.load(qrows, orows, r0 + TILE);
+    if (ntiles > 1) {
+      st.load(qrows, orows, qstart + TILE);
+      if (threadIdx.x < TILE) stats_load(qstart + TILE, lnext, dnext);
+    }
+  }
+  __syncthreads();
+  for (int it = 0; it < ntiles; it++) {
+    const int r0 = qstart + it * TILE, buf = it & 1;
+    const u16* Qb = Qs[buf];
+    const u16* Ob = Os[buf];
+    const float* Lb = Ls[buf];
+    const float* Db = Ds[buf];
 #pragma unroll
     for (int sub = 0; sub < 2; sub++) {
       const int s0 = r0 + sub * 32;
@@ -514,40 +563,60 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_mfma(const u16* __rest
         s[t] = zero16();
         dp[t] = zero16();
       }
+      // one wave per SIMD: nothing else hides LDS latency, so every fragment of the half is read
+      // before the MFMA chains that use them
+      u16x8 qa[D / 16], oa[D / 16];
 #pragma unroll
       for (int ds = 0; ds < D / 16; ds++) {
-        const u16x8 a = *(const u16x8*)(Qs + (sub * 32 + n) * RS + ds * 16 + 8 * h);
-        const u16x8 e = *(const u16x8*)(Os + (sub * 32 + n) * RS + ds * 16 + 8 * h);
+        qa[ds] = read_row<D>(Qb, sub * 32 + n, 2 * ds + h);
+        oa[ds] = read_row<D>(Ob, sub * 32 + n, 2 * ds + h);
+      }
+#pragma unroll
+      for (int ds = 0; ds < D / 16; ds++)
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-          s[t] = T::mfma32(a, kf[t][ds], s[t]);
-          dp[t] = T::mfma32(e, vf[t][ds], dp[t]);
+          s[t] = T::mfma32(qa[ds], kf[t][ds], s[t]);
+          dp[t] = T::mfma32(oa[ds], vf[t][ds], dp[t]);
         }
-      }
+      // the transposed fragments of both k-chunks, in flight during the softmax arithmetic
+      u16x8 ot[2][D / 32], qt[2][D / 32];
+#pragma unroll
+      for (int c = 0; c < 2; c++)
+#pragma unroll
+        for (int dt = 0; dt < D / 32; dt++) {
+          ot[c][dt] = read_transposed<D>(Ob, sub * 32 + 16 * c, dt * 32);
+          qt[c][dt] = read_transposed<D>(Qb, sub * 32 + 16 * c, dt * 32);
+        }
       const bool edge = (s0 + 32 > t_q) || MASK || (CAUSAL && s0 < wk0 + 32 * NT - 1);
+      // the statistics of the half's queries (item i <-> query rb(i / 4) + i % 4), the
+      // probabilities, the masking as one uniform block of selects, then dS
+      f32x4 l4[4], d4[4];
 #pragma unroll
       for (int g = 0; g < 4; g++) {
-        const int rb = sub * 32 + 8 * g + 4 * h;
-        const f32x4 l4 = *(const f32x4*)(Ls + rb);
-        const f32x4 d4 = *(const f32x4*)(Ds + rb);
+        l4[g] = *(const f32x4*)(Lb + sub * 32 + 8 * g + 4 * h);
+        d4[g] = *(const f32x4*)(Db + sub * 32 + 8 * g + 4 * h);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) s[t][i] = fast_exp2(fmaf(s[t][i], c2, -l4[i >> 2][i & 3]));
+      if (edge) {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
           const int key = wk0 + 32 * t + n;
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const int i = 4 * g + e;
-            float p = fast_exp2(fmaf(s[t][i], c2, -l4[e]));
-            if (edge) {
-              const int qq = r0 + rb + e;
-              bool hide = (qq >= t_q) | !live[t];
-              if (CAUSAL) hide |= qq < key;
-              p = hide ? 0.f : p;
-            }
-            s[t][i] = p;
-            dp[t][i] = p * (dp[t][i] - d4[e]) * scale;
+          for (int i = 0; i < 16; i++) {
+            const int qq = s0 + 8 * (i >> 2) + 4 * h + (i & 3);
+            bool hide = (qq >= t_q) | !live[t];
+            if (CAUSAL) hide |= qq < key;
+            s[t][i] = hide ? 0.f : s[t][i];
           }
         }
       }
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) dp[t][i] = s[t][i] * fmaf(dp[t][i], scale, -d4[i >> 2][i & 3]);
 #pragma unroll
       for (int c = 0; c < 2; c++) {
         u16x8 pb[NT], gb[NT];
@@ -557,18 +626,26 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_mfma(const u16* __rest
           gb[t] = pack8<T>(dp[t], 8 * c);
         }
 #pragma unroll
-        for (int dt = 0; dt < D / 32; dt++) {
-          const int d = dt * 32 + n, pos = trot(d, sub * 32 + 16 * c + 8 * h);
-          const u16x8 a = *(const u16x8*)(Ot + d * CS + pos);
-          const u16x8 e = *(const u16x8*)(Qt + d * CS + pos);
+        for (int dt = 0; dt < D / 32; dt++)
 #pragma unroll
           for (int t = 0; t < NT; t++) {
-            gv[t][dt] = T::mfma32(a, pb[t], gv[t][dt]);
-            gk[t][dt] = T::mfma32(e, gb[t], gk[t][dt]);
+            gv[t][dt] = T::mfma32(ot[c][dt], pb[t], gv[t][dt]);
+            gk[t][dt] = T::mfma32(qt[c][dt], gb[t], gk[t][dt]);
           }
-        }
       }
     }
+    if (it + 1 < ntiles) {
+      st.store(Qs[buf ^ 1], Os[buf ^ 1]);
+      if (threadIdx.x < TILE) {
+        Ls[buf ^ 1][threadIdx.x] = lnext;
+        Ds[buf ^ 1][threadIdx.x] = dnext;
+      }
+      if (it + 2 < ntiles) {
+        st.load(qrows, orows, r0 + 2 * TILE);
+        if (threadIdx.x < TILE) stats_load(r0 + 2 * TILE, lnext, dnext);
+      }
+    }
+    __syncthreads();
   }
 #pragma unroll
   for (int t = 0; t < NT; t++) {
@@ -584,8 +661,11 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_mfma(const u16* __rest
 // MFMAs) wherever the accumulators still fit the register file.
 template <int D>
 constexpr int tiles_per_wave(SdpaPass pass) {
-  if (pass == SDPA_FWD) return 1;  // two workgroups per CU hide its latency better than operand reuse
-  return (pass == SDPA_BWD_KV && D == 128) ? 1 : 2;
+  // at D = 128 the forward and dQ pass run two workgroups per CU (two waves per SIMD), which
+  // hides their latency better than operand reuse; the dK/dV pass's four accumulator sets fill
+  // the register file at one tile
+  if (D == 128 || pass == SDPA_FWD) return 1;
+  return 2;
 }
 
 template <typename T, int D, int NT, bool CAUSAL, bool MASK, SdpaPass PASS>
