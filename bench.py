@@ -15,8 +15,15 @@ dK), sdpa_bwd_q 1U (dQ; its recomputed S and dP are executed, not algorithmic).
 
 Timing: W untimed warmup steps, then K steps between two hipEvents on the null stream with a
 device synchronize on both sides; per-kernel averages come from events recorded between the
-launches of every timed step. The CPU baseline is the oracle's numpy flash attention (a port of
-limn/sdpa.py) on one (b, h) pair of the same inputs, scaled to all B*H pairs.
+launches of every timed step.
+
+CPU baseline (`cpu_baseline`): oracle/c_device.py, limn's single-threaded C backend restated
+over this package's loop-nest IR (reference limn/backend_c.py), timed inside its compiled nests
+on one host core. It declines bfloat16 as the reference does, so C3 and C4 run float32 twins; it
+has no CUSTOM kernels, so attention takes limn's composed path, on one of the B*H (b, h) pairs,
+scaled to all of them. `cpu_numpy_oracle` adds the numpy flash attention of the oracle (a port of
+limn/sdpa.py) on the same pair. `workloads` carries C1, C2 and C3, each with its own roofline
+and CPU baseline line.
 """
 
 from __future__ import annotations
@@ -56,7 +63,7 @@ def parse() -> argparse.Namespace:
     p.add_argument(
         "--workload",
         default="c4",
-        choices=["c4", "copy", "c2", "c3"],
+        choices=["c4", "copy", "c1", "c2", "c3"],
         help="c4: the headline attention step; copy: a plain 256 MiB device copy kernel, the "
         "known-size reference that scales rocprofv3's FETCH_SIZE/WRITE_SIZE counters",
     )
@@ -120,6 +127,49 @@ class Events:
         return float(out.value)
 
 
+def c_device_run(build) -> float:
+    """Seconds spent inside the compiled nests when the graph `build()` returns (a list of
+    tensors) is realized on the CPU baseline: oracle/c_device.py, limn's single-threaded C backend
+    restated over this package's IR. Plan building and compiling are not timed."""
+    from limn_amd import device as limn_device
+    from oracle.c_device import CDevice
+
+    saved = limn_device.active_device
+    dev = CDevice()
+    limn_device.active_device = dev
+    try:
+        tensors = build()
+        dev.execute([t.node for t in tensors])
+    finally:
+        limn_device.active_device = saved
+    return dev.seconds
+
+
+def c4_cpu_baseline(host, scale: float, B: int, H: int, units: float) -> dict:
+    """The C device on one (b, h) pair of the same inputs as float32 (it declines bfloat16, like
+    the reference's): limn's composed causal attention, forward and backward through the Tensor
+    API, as the reference's C backend runs it (no CUSTOM kernels). Scaled to all B*H pairs."""
+    from limn_amd.dtypes import bf16_values
+    from limn_amd.tensor import Tensor, grad
+
+    q, k, v, do = (bf16_values(h.reshape(B, H, -1, h.shape[-1])[:1, :1]).astype(np.float32) for h in host)
+
+    def build():
+        Q, K, V = (Tensor(x, requires_grad=True) for x in (q, k, v))
+        out = Q.attention(K, V, causal=True)
+        return [out, *grad((out * Tensor(do)).sum(), [Q, K, V])]
+
+    one = c_device_run(build)
+    return {
+        "value": round(units / (one * B * H) / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"C device (limn/backend_c.py restated, gcc -O3, 1 thread), float32 twin, composed causal attention "
+        f"fwd+bwd on 1 of {B * H} (b,h) pairs: {one:.2f} s in compiled nests, scaled x{B * H}",
+    }
+
+
 def cpu_baseline(q, k, v, do, scale: float, B: int, H: int, units: float) -> dict:
     """The oracle's numpy flash attention (port of limn/sdpa.py) on one (b, h) pair, f32 work,
     the reference's default block size 16, scaled by B*H."""
@@ -175,7 +225,7 @@ def timed_calls(dev, plan, sources, ev: Events, base: int) -> int:
     return base + len(plan.calls) + 1
 
 
-def bench_c2(dev, steps: int, warmup: int) -> dict:
+def bench_c2(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     """x f32 (8192, 8192) ~ N(0,1) from default_rng(2); row softmax then
     LayerNorm (gamma 1, beta 0, eps 1e-5), fused by the scheduler into its 11 kernels and
     emitted by the hip device. Reports the chain's algorithmic GB/s and each kernel's."""
@@ -223,6 +273,15 @@ def bench_c2(dev, steps: int, warmup: int) -> dict:
         kernels.append({"ms": round(float(per[i]), 4), "bytes": moved, "GB_s": round(moved / (per[i] * 1e-3) / 1e9, 1)})
     dom = int(np.argmax(per))
     achieved = kernels[dom]["bytes"] / (per[dom] * 1e-3)
+
+    def build():
+        x = Tensor(np.random.default_rng(2).standard_normal((N, N), dtype=np.float32))
+        y = x.softmax(-1)
+        c = y - y.mean(axis=-1, keepdim=True)
+        var = (c * c).mean(axis=-1, keepdim=True)
+        return [c / (var + 1e-5).sqrt() * Tensor.ones((N,)) + Tensor.zeros((N,))]
+
+    cpu_s = c_device_run(build) if with_cpu else None
     return {
         "metric": "fused-kernel HBM GB/s",
         "value": round(total / (chain_ms * 1e-3) / 1e9, 1),
@@ -240,15 +299,22 @@ def bench_c2(dev, steps: int, warmup: int) -> dict:
             "frac": round(achieved / HBM_PEAK, 4),
             "traffic": traffic(f"c2:k{dom}"),
         },
+        "cpu_baseline": None if cpu_s is None else {
+            "value": round(total / cpu_s / 1e9, 3),
+            "unit": "GB/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"C device (limn/backend_c.py restated, gcc -O3, 1 thread), the same 11 kernels at full size: {cpu_s:.2f} s",
+        },
     }
 
 
-def bench_c3(dev, steps: int, warmup: int) -> dict:
+def bench_c3(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     """bf16 A(4096x4096) @ B(4096x4096) with f32 accumulate, relu and a bf16
     store; A, B ~ N(0, 0.125^2) from default_rng(3). The scheduler gives two nests (the SUM
     contraction, which the device lowers to its MFMA kernel, and the relu); both are timed."""
     from limn_amd import device as limn_device
-    from limn_amd.dtypes import bf16_bits
+    from limn_amd.dtypes import bf16_bits, bf16_values
     from limn_amd.ops import bfloat16
     from limn_amd.tensor import Tensor
 
@@ -274,6 +340,15 @@ def bench_c3(dev, steps: int, warmup: int) -> dict:
     per /= steps
     flops = 2.0 * n**3
     mm = float(per[0])
+    rows = 512  # the CPU leg multiplies a 512-row slice of A (1/8 of the work) and scales
+
+    def build():
+        r2 = np.random.default_rng(3)
+        a32 = bf16_values(bf16_bits(r2.standard_normal((n, n), dtype=np.float32) * 0.125))[:rows].astype(np.float32)
+        b32 = bf16_values(bf16_bits(r2.standard_normal((n, n), dtype=np.float32) * 0.125)).astype(np.float32)
+        return [(Tensor(a32) @ Tensor(b32)).relu()]
+
+    cpu_s = c_device_run(build) if with_cpu else None
     return {
         "metric": "matmul TFLOP/s",
         "value": round(flops / (float(per.sum()) * 1e-3) / 1e12, 2),
@@ -291,6 +366,90 @@ def bench_c3(dev, steps: int, warmup: int) -> dict:
             "frac": round(flops / (mm * 1e-3) / MFMA_BF16_PEAK, 4),
             "traffic": traffic("c3:matmul_mfma<BF16,256,256,true,false,0>"),
         },
+        "cpu_baseline": None if cpu_s is None else {
+            "value": round(2.0 * rows * n * n / cpu_s / 1e12, 6),
+            "unit": "TFLOP/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"C device (limn/backend_c.py restated, gcc -O3, 1 thread), float32 twin, (A[:{rows}] @ B).relu(): {cpu_s:.2f} s",
+        },
+    }
+
+
+def bench_c1(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
+    """causal sdpa f32, q, k, v, dO (2, 4, 256, 64) ~ N(0,1) from
+    default_rng(1), scale 1/8; one step is the forward and both backward passes (the general-width
+    kernels: f32 has no MFMA path). Launch-latency bound: reported in microseconds and as
+    FlashAttention-convention flop/s against the f32 peak."""
+    from limn_amd.ops import Node, Op, custom, float32
+    from limn_amd.tensor import Tensor, grad
+
+    B, H, S, D = 2, 4, 256, 64
+    scale = D**-0.5
+    r = np.random.default_rng(1)
+    host = [r.standard_normal((B, H, S, D), dtype=np.float32) for _ in range(4)]
+
+    def buffer(arr, shape):
+        buf = dev.alloc(arr.nbytes)
+        dev.copyin(buf, arr)
+        return Node(Op.BUFFER, (), float32, shape, buf)
+
+    q, k, v, do = (buffer(a, (B, H, S, D)) for a in host)
+    o_node, _ = custom("sdpa", (q, k, v), (True, scale), ((float32, (B, H, S, D)), (float32, (B, H, S, 1))))
+    fwd = dev.custom_runner(o_node)
+    out, lse = dev.out_alloc(B * H * S * D * 4, False), dev.out_alloc(B * H * S * 4, False)
+    fwd([q.arg, k.arg, v.arg], [out, lse])
+    dev.finish()
+    o_host = dev.copyout(out).view(np.float32).reshape(B, H, S, D)
+    delta = buffer((host[3] * o_host).sum(axis=-1, keepdims=True).astype(np.float32), (B, H, S, 1))
+    lse_node = Node(Op.BUFFER, (), float32, (B, H, S, 1), lse)
+    srcs = (q, k, v, do, lse_node, delta)
+    (dq_node,) = custom("sdpa_bwd_q", srcs, (True, scale), ((float32, (B, H, S, D)),))
+    dk_node, _ = custom("sdpa_bwd_kv", srcs, (True, scale), ((float32, (B, H, S, D)), (float32, (B, H, S, D))))
+    bwd_q, bwd_kv = dev.custom_runner(dq_node), dev.custom_runner(dk_node)
+    dq, dk, dv = (dev.out_alloc(B * H * S * D * 4, False) for _ in range(3))
+    ins_fwd, ins_bwd = [q.arg, k.arg, v.arg], [q.arg, k.arg, v.arg, do.arg, lse, delta.arg]
+
+    def step():
+        fwd(ins_fwd, [out, lse])
+        bwd_q(ins_bwd, [dq])
+        bwd_kv(ins_bwd, [dk, dv])
+
+    for _ in range(warmup):
+        step()
+    dev.finish()
+    ev = Events(dev.api, 2)
+    ev.record(0)
+    for _ in range(steps):
+        step()
+    ev.record(1)
+    dev.finish()
+    us = ev.ms(0, 1) / steps * 1e3
+    flops = 7 * (2.0 * B * H * S * S * D / 2)  # 2.35e8: fwd 2U + bwd 5U, causal counted as half
+
+    def build():
+        Q, K, V = (Tensor(x, requires_grad=True) for x in host[:3])
+        o = Q.attention(K, V, causal=True)
+        return [o, *grad((o * Tensor(host[3])).sum(), [Q, K, V])]
+
+    cpu_s = c_device_run(build) if with_cpu else None
+    return {
+        "metric": "sdpa fwd+bwd microseconds per step",
+        "value": round(us, 2),
+        "unit": "us",
+        "higher_is_better": False,
+        "dtype": "f32",
+        "config": {"workload": "C1 causal sdpa f32 B2 H4 S256 D64, fwd + bwd (general-width kernels)", "flop_per_step": flops},
+        "tflops": round(flops / (us * 1e-6) / 1e12, 3),
+        "roofline": {"kernel": "sdpa (all three passes)", "bound": "latency", "achieved": round(flops / (us * 1e-6) / 1e12, 3),
+                     "peak": 157.3, "unit": "TFLOP/s", "frac": round(flops / (us * 1e-6) / 157.3e12, 5), "traffic": None},
+        "cpu_baseline": None if cpu_s is None else {
+            "value": round(cpu_s * 1e6, 1),
+            "unit": "us",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"C device (limn/backend_c.py restated, gcc -O3, 1 thread), composed causal attention fwd+bwd, full C1: {cpu_s * 1e3:.1f} ms",
+        },
     }
 
 
@@ -302,15 +461,20 @@ def main() -> int:
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     if args.workload == "copy":
         return copy_probe(args.steps)
+    if args.workload == "c1":
+        from limn_amd.hip.device import HipDevice
+
+        print(json.dumps(bench_c1(HipDevice(), args.steps, args.warmup, not args.no_cpu)), flush=True)
+        return 0
     if args.workload == "c2":
         from limn_amd.hip.device import HipDevice
 
-        print(json.dumps(bench_c2(HipDevice(), args.steps, args.warmup)), flush=True)
+        print(json.dumps(bench_c2(HipDevice(), args.steps, args.warmup, not args.no_cpu)), flush=True)
         return 0
     if args.workload == "c3":
         from limn_amd.hip.device import HipDevice
 
-        print(json.dumps(bench_c3(HipDevice(), args.steps, args.warmup)), flush=True)
+        print(json.dumps(bench_c3(HipDevice(), args.steps, args.warmup, not args.no_cpu)), flush=True)
         return 0
     from limn_amd.dtypes import bf16_bits, bf16_values
     from limn_amd.hip.device import HipDevice
@@ -427,10 +591,16 @@ def main() -> int:
         "device": {"arch": dev.arch, "compute_units": dev.compute_units},
     }
     if not args.no_cpu:
+        line["cpu_baseline"] = c4_cpu_baseline(host, scale, B, H, step_flops)
         inputs = [bf16_values(h.reshape(B, H, S, D)[:1, :1]) for h in host]
-        line["cpu_baseline"] = cpu_baseline(*inputs, scale, B, H, step_flops)
+        line["cpu_numpy_oracle"] = cpu_baseline(*inputs, scale, B, H, step_flops)
     del q, k, v, do, out, lse, dq, dk, dv, delta, lse_node, o_node, l_node, dq_node, dk_node
-    line["workloads"] = {"C2": bench_c2(dev, args.steps, args.warmup), "C3": bench_c3(dev, args.steps, args.warmup)}
+    cpu = not args.no_cpu
+    line["workloads"] = {
+        "C1": bench_c1(dev, args.steps, args.warmup, cpu),
+        "C2": bench_c2(dev, args.steps, args.warmup, cpu),
+        "C3": bench_c3(dev, args.steps, args.warmup, cpu),
+    }
     print(json.dumps(line), flush=True)
     return 0
 
