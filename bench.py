@@ -63,7 +63,7 @@ def parse() -> argparse.Namespace:
     p.add_argument(
         "--workload",
         default="c4",
-        choices=["c4", "copy", "c1", "c2", "c3"],
+        choices=["c4", "copy", "c1", "c2", "c3", "c5"],
         help="c4: the headline attention step; copy: a plain 256 MiB device copy kernel, the "
         "known-size reference that scales rocprofv3's FETCH_SIZE/WRITE_SIZE counters",
     )
@@ -453,6 +453,82 @@ def bench_c1(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     }
 
 
+def bench_c5(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
+    """one training step of the byte-level GPT (vocab 256, d 512, 8 layers,
+    8 heads, ctx 512, batch 32, tanh GELU, bf16 activations over float32 masters, AdamW lr 3e-4
+    wd 0.1), random init from seed 5, tokens uniform in [0, 256) from default_rng(5). The step is
+    captured (limn_amd.capture) and replayed; a step is forward, backward and the AdamW update
+    committed with the loss, one plan transaction ending in one device synchronize, so wall time
+    around K replays is the whole job's (kernel time plus host launch time)."""
+    from limn_amd import device as limn_device
+    from limn_amd.capture import capture
+    from limn_amd.gpt import GPTConfig, make_trainer, synthetic_batch
+    from limn_amd.ops import float32
+    from limn_amd.tensor import set_seed
+
+    cfg = GPTConfig()
+    saved = limn_device.active_device
+    limn_device.active_device = dev
+    try:
+        set_seed(5)
+        _, _, step = make_trainer(cfg)
+        fn = capture(step)
+        rng = np.random.default_rng(5)
+        batches = [synthetic_batch(cfg, rng) for _ in range(4)]
+        for i in range(max(warmup, 3)):  # two observed calls, then replays
+            loss = fn(*batches[i % 4])
+        first_loss = float(loss.item())
+        dev.finish()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            loss = fn(*batches[i % 4])
+        dev.finish()
+        elapsed = time.perf_counter() - t0
+        last_loss = float(loss.item())
+    finally:
+        limn_device.active_device = saved
+    per_step = cfg.flops_per_token() * cfg.tokens
+    tok_s = steps * cfg.tokens / elapsed
+
+    cpu = None
+    if with_cpu:
+        from limn_amd import device as limn_device2
+        from oracle.c_device import CDevice
+
+        twin = GPTConfig(batch=1, dtype=float32)
+        cdev = CDevice()
+        limn_device2.active_device = cdev
+        try:
+            set_seed(5)
+            _, _, cstep = make_trainer(twin)
+            cstep(*synthetic_batch(twin, np.random.default_rng(5)))
+        finally:
+            limn_device2.active_device = saved
+        cpu = {
+            "value": round(twin.tokens / cdev.seconds, 2),
+            "unit": "tok/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"C device (limn/backend_c.py restated, gcc -O3, 1 thread), float32 twin, one training step of "
+            f"batch 1 ({twin.tokens} tokens, composed attention): {cdev.seconds:.1f} s in compiled nests",
+        }
+    return {
+        "metric": "GPT training step tok/s",
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "ms_per_step": round(elapsed / steps * 1e3, 3),
+        "dtype": "bf16",
+        "config": {"workload": "C5 byte-level GPT training step (captured), d512 L8 H8 ctx512 batch32, AdamW",
+                   "tokens_per_step": cfg.tokens, "flop_per_step": per_step, "params_in_matmuls": cfg.matmul_params()},
+        "mfu": round(per_step * steps / elapsed / MFMA_BF16_PEAK, 4),
+        "loss": {"after_warmup": round(first_loss, 4), "last": round(last_loss, 4)},
+        "roofline": {"kernel": "whole step", "bound": "mfma", "achieved": round(per_step * steps / elapsed / 1e12, 2),
+                     "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s", "frac": round(per_step * steps / elapsed / MFMA_BF16_PEAK, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+    }
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -465,6 +541,11 @@ def main() -> int:
         from limn_amd.hip.device import HipDevice
 
         print(json.dumps(bench_c1(HipDevice(), args.steps, args.warmup, not args.no_cpu)), flush=True)
+        return 0
+    if args.workload == "c5":
+        from limn_amd.hip.device import HipDevice
+
+        print(json.dumps(bench_c5(HipDevice(), args.steps, args.warmup, not args.no_cpu)), flush=True)
         return 0
     if args.workload == "c2":
         from limn_amd.hip.device import HipDevice
@@ -600,6 +681,7 @@ def main() -> int:
         "C1": bench_c1(dev, args.steps, args.warmup, cpu),
         "C2": bench_c2(dev, args.steps, args.warmup, cpu),
         "C3": bench_c3(dev, args.steps, args.warmup, cpu),
+        "C5": bench_c5(dev, min(args.steps, 10), min(args.warmup, 3), cpu),
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -339,11 +339,27 @@ def _flat_stride(coeffs: dict[str, int], batch_vars: list[tuple[str, int]]) -> i
     return stride
 
 
+def _flat_reduce(inner: list[tuple[str, int]], ta: dict[str, int], tb: dict[str, int]) -> tuple[int, int, int] | None:
+    """Several reduce vars as one k: both operands must step through them as one row-major
+    index (each var's stride the next one's extent times its stride, in the same order for both),
+    as a weight gradient's sum over (batch, time) does. Returns (K, k stride in a, in b)."""
+    extent = dict(inner)
+    if any(v not in ta or v not in tb or ta[v] <= 0 or tb[v] <= 0 for v in extent):
+        return None
+    order = sorted(extent, key=lambda v: -ta[v])
+    for outer, nxt in zip(order, order[1:]):
+        if ta[outer] != extent[nxt] * ta[nxt] or tb[outer] != extent[nxt] * tb[nxt]:
+            return None
+    last = order[-1]
+    return math.prod(extent.values()), ta[last], tb[last]
+
+
 def find_contraction(nest: LoopNest, shape: NestShape) -> Contraction | None:
     """The dense-contraction reading of a reduce nest (reference limn/cuda_emit.py:376-505
-    detects the same shape): one reduce var, a body of exactly two unmasked loads and their
-    product, each load depending on the reduce var, the batch vars and one row var of its own."""
-    if shape.fold is not Op.ADD or len(shape.inner) != 1 or len(shape.body) != 3:
+    detects the same shape, over one reduce var): a body of exactly two unmasked loads and their
+    product, each load depending on every reduce var (flattened into one k, see _flat_reduce),
+    the batch vars and one row var of its own."""
+    if shape.fold is not Op.ADD or not shape.inner or len(shape.body) != 3:
         return None
     loads = [i for i in shape.body if i.opcode is Opcode.LOAD]
     mul = [i for i in shape.body if i.opcode is Opcode.ARITH and i.arg is Op.MUL]
@@ -356,11 +372,12 @@ def find_contraction(nest: LoopNest, shape: NestShape) -> Contraction | None:
         return None
     if nest.kernel.target.dtype != dtype:
         return None
-    r, K = shape.inner[0]
     kept = sorted(shape.outer, key=lambda ve: int(ve[0][1:]))
     ta, tb = dict(loads[0].arg[1].terms), dict(loads[1].arg[1].terms)
-    if r not in ta or r not in tb:
+    reduce = _flat_reduce(shape.inner, ta, tb)
+    if reduce is None:
         return None
+    K, red_a, red_b = reduce
     only_a = [v for v, _ in kept if v in ta and v not in tb]
     only_b = [v for v, _ in kept if v in tb and v not in ta]
     if not only_a or not only_b:
@@ -377,7 +394,7 @@ def find_contraction(nest: LoopNest, shape: NestShape) -> Contraction | None:
     batch = math.prod(e for _, e in batch_vars)
     M, N = extent[m_var], extent[n_var]
     a_in, b_in = int(loads[0].arg[0][2:]), int(loads[1].arg[0][2:])
-    a_m, a_k, b_n, b_k = ta[m_var], ta[r], tb[n_var], tb[r]
+    a_m, a_k, b_n, b_k = ta[m_var], red_a, tb[n_var], red_b
     c_m, c_n = tc[m_var], tc[n_var]
     if batch > 1 and b_b == 0 and a_b == M * a_m and c_b == M * c_m:
         M, batch, a_b, c_b = M * batch, 1, 0, 0  # a shared right operand: one taller contraction

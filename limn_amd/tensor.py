@@ -472,8 +472,13 @@ class Tensor:
             raise ValueError(f"matmul: inner dims differ, {a.shape} @ {b.shape}")
         batch = broadcast_shape(a.shape[:-2], b.shape[:-2], "matmul")
         m, k, n = a.shape[-2], a.shape[-1], b.shape[-1]
-        a = broadcast_to(a, batch + a.shape[-2:], "matmul").reshape(*batch, m, 1, k).expand(*batch, m, n, k)
-        b = broadcast_to(b, batch + b.shape[-2:], "matmul").transpose(-2, -1).reshape(*batch, 1, n, k).expand(*batch, m, n, k)
+        # each operand is lifted to full rank with size-1 dims and expanded once, so its gradient
+        # is one sum over every broadcast axis (a weight's over batch and rows together: one
+        # contraction) rather than a sum per axis
+        lead_a = (1,) * (len(batch) - len(a.shape[:-2])) + a.shape[:-2]
+        lead_b = (1,) * (len(batch) - len(b.shape[:-2])) + b.shape[:-2]
+        a = a.reshape(*lead_a, m, 1, k).expand(*batch, m, n, k)
+        b = b.transpose(-2, -1).reshape(*lead_b, 1, n, k).expand(*batch, m, n, k)
         return (a * b).sum(axis=-1)
 
     def __matmul__(self, other: Tensor) -> Tensor:
