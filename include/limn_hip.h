@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LIMN_HIP_ABI_VERSION 1
+#define LIMN_HIP_ABI_VERSION 2
 
 enum {
   LIMN_HIP_FLOAT64 = 0,
@@ -95,10 +95,19 @@ int limn_hip_sdpa_bwd_kv(const void* q, const void* k, const void* v, const void
  * contiguous along k or along its row (m / n) with the other stride a multiple of 8.
  * epilogue: 0 = none, 1 = relu before the store. Replaces the tiled SIMT matmul the reference
  * emits for a dense contraction nest, limn/cuda_emit.py:376-685 (matmul_shape, emit_tiled).
+ * A contraction with too few output tiles to fill the GPU and a long k (a weight gradient: a sum
+ * over every batch row) splits k: float32 partial tiles go to `workspace` and a second kernel adds
+ * them in a fixed order, so results are deterministic. `workspace` must hold
+ * limn_hip_matmul_workspace(...) bytes for that; with a null or smaller workspace the
+ * contraction runs unsplit (same result, slower).
  */
 int limn_hip_matmul(const void* a, const void* b, void* c, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
                     int64_t a_batch, int64_t a_m, int64_t a_k, int64_t b_batch, int64_t b_k, int64_t b_n, int64_t c_batch,
-                    int64_t c_m, int64_t c_n, int epilogue, void* stream);
+                    int64_t c_m, int64_t c_n, int epilogue, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Bytes of workspace limn_hip_matmul uses to split k for this shape; 0 when it does not split. No
+ * counterpart in the reference (its contraction kernel never splits). */
+int64_t limn_hip_matmul_workspace(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K);
 
 /* 1 when limn_hip_matmul has a kernel for this dtype and operand layout, else 0 (the device
  * then keeps the contraction on the general reduce kernels). */

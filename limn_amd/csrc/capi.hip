@@ -125,7 +125,7 @@ int limn_hip_sdpa_bwd_kv(const void* q, const void* k, const void* v, const void
 
 int limn_hip_matmul(const void* a, const void* b, void* c, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
                     int64_t a_batch, int64_t a_m, int64_t a_k, int64_t b_batch, int64_t b_k, int64_t b_n, int64_t c_batch,
-                    int64_t c_m, int64_t c_n, int epilogue, void* stream) {
+                    int64_t c_m, int64_t c_n, int epilogue, void* workspace, int64_t workspace_bytes, void* stream) {
   MatmulShape s = {batch, M, N, K, a_batch, a_m, a_k, b_batch, b_k, b_n, c_batch, c_m, c_n};
   if (dtype != LIMN_HIP_BFLOAT16 && dtype != LIMN_HIP_FLOAT16)
     return fail(LIMN_HIP_EUNSUPPORTED, "matmul: the MFMA contraction takes bfloat16 or float16, not dtype code %d", dtype);
@@ -138,7 +138,14 @@ int limn_hip_matmul(const void* a, const void* b, void* c, int dtype, int64_t ba
   if (!matmul_layout_ok(s))
     return fail(LIMN_HIP_EUNSUPPORTED, "matmul: operands must be contiguous along m/n or k with 16-byte aligned rows");
   if (((uintptr_t)a | (uintptr_t)b) % 16 != 0) return fail(LIMN_HIP_EUNSUPPORTED, "matmul: operands must be 16-byte aligned");
-  return launch_matmul(a, b, c, dtype, s, epilogue, (hipStream_t)stream);
+  if (workspace_bytes < 0) return fail(LIMN_HIP_EINVAL, "matmul: negative workspace size");
+  return launch_matmul(a, b, c, dtype, s, epilogue, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int64_t limn_hip_matmul_workspace(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K) {
+  if ((dtype != LIMN_HIP_BFLOAT16 && dtype != LIMN_HIP_FLOAT16) || batch < 1 || M < 1 || N < 1 || K < 1) return 0;
+  MatmulShape s = {batch, M, N, K, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  return matmul_workspace_bytes(s);
 }
 
 int limn_hip_matmul_supported(int dtype, int64_t M, int64_t N, int64_t K, int64_t a_batch, int64_t a_m, int64_t a_k,

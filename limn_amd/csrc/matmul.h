@@ -15,8 +15,17 @@ struct MatmulShape {
 
 enum { MATMUL_EPILOGUE_NONE = 0, MATMUL_EPILOGUE_RELU = 1 };
 
+// How a contraction is cut: output tiles of `tile` x `tile`, k in `split` slices of `chunk`.
+struct MatmulPlan {
+  int tile;
+  int64_t split, chunk;
+};
+MatmulPlan plan_matmul(const MatmulShape& s);
+int64_t matmul_workspace_bytes(const MatmulShape& s);
+
 // 1 when every operand is contiguous along one of its two dims with 16-byte aligned rows.
 int matmul_layout_ok(const MatmulShape& s);
-int launch_matmul(const void* a, const void* b, void* c, int dtype, const MatmulShape& s, int epilogue, hipStream_t stream);
+int launch_matmul(const void* a, const void* b, void* c, int dtype, const MatmulShape& s, int epilogue, void* workspace,
+                  int64_t workspace_bytes, hipStream_t stream);
 
 }  // namespace limn

@@ -13,6 +13,12 @@
 // K advances BK = 64 per stage through a double-buffered LDS: the next stage's global loads are
 // in registers while the current stage is multiplied.
 //
+// Split k: a contraction whose output has too few tiles to give every CU a workgroup and whose k
+// is long (a weight gradient sums over all batch rows) is cut into k slices; each workgroup
+// computes one tile over one slice and writes float32 partials, and matmul_splits adds the
+// slices per element in slice order, applies the epilogue and rounds, so the result does not
+// depend on scheduling.
+//
 // LDS holds both operands k-contiguous (A as [m][k], B as [n][k], rows padded by 8 elements
 // so 16-byte reads across a 32-row operand are conflict-free), so each MFMA operand is one
 // ds_read_b128. An operand that is k-contiguous in memory is staged with 16-byte row loads;
@@ -117,9 +123,10 @@ struct OperandStage {
   }
 };
 
-template <typename T, int BM, int BN, bool A_K, bool B_K, int EPI>
+template <typename T, int BM, int BN, bool A_K, bool B_K, int EPI, bool PARTIAL>
 __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restrict__ a, const u16* __restrict__ b,
-                                                             u16* __restrict__ c, MatmulShape s) {
+                                                             u16* __restrict__ c, float* __restrict__ ws, MatmulShape s,
+                                                             int64_t chunk) {
   constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 accumulators per wave along m and n
   __shared__ __attribute__((aligned(16))) u16 As[2][BM * LS];
   __shared__ __attribute__((aligned(16))) u16 Bs[2][BN * LS];
@@ -127,9 +134,11 @@ __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restri
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n32 = lane & 31;
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t tiles_n = (s.N + BN - 1) / BN, tiles_m = (s.M + BM - 1) / BM;
-  const int64_t per_batch = tiles_m * tiles_n;
-  const int64_t bz = blockIdx.x / per_batch;
-  const int64_t t = blockIdx.x - bz * per_batch;
+  const int64_t per_batch = tiles_m * tiles_n, per_slice = s.batch * per_batch;
+  const int64_t slice = blockIdx.x / per_slice;  // 0 unless k is split
+  const int64_t bz = (blockIdx.x - slice * per_slice) / per_batch;
+  const int64_t t = blockIdx.x - slice * per_slice - bz * per_batch;
+  const int64_t k_lo = slice * chunk, k_hi = k_lo + chunk < s.K ? k_lo + chunk : s.K;
   const int64_t tm = t / tiles_n, tn = t - tm * tiles_n;
   const int64_t m0 = tm * BM, n0 = tn * BN;
   const u16* abase = a + bz * s.a_batch;
@@ -147,17 +156,17 @@ __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restri
   OperandStage<BN, B_K> sb;
   const int64_t a_stride = A_K ? s.a_m : s.a_k;
   const int64_t b_stride = B_K ? s.b_n : s.b_k;
-  const int stages = (int)((s.K + BK - 1) / BK);
-  sa.load(abase, m0, s.M, 0, s.K, a_stride);
-  sb.load(bbase, n0, s.N, 0, s.K, b_stride);
+  const int stages = (int)((k_hi - k_lo + BK - 1) / BK);
+  sa.load(abase, m0, s.M, k_lo, k_hi, a_stride);
+  sb.load(bbase, n0, s.N, k_lo, k_hi, b_stride);
   sa.store(As[0]);
   sb.store(Bs[0]);
   __syncthreads();
   for (int st = 0; st < stages; st++) {
     const int cur = st & 1;
     if (st + 1 < stages) {
-      sa.load(abase, m0, s.M, (int64_t)(st + 1) * BK, s.K, a_stride);
-      sb.load(bbase, n0, s.N, (int64_t)(st + 1) * BK, s.K, b_stride);
+      sa.load(abase, m0, s.M, k_lo + (int64_t)(st + 1) * BK, k_hi, a_stride);
+      sb.load(bbase, n0, s.N, k_lo + (int64_t)(st + 1) * BK, k_hi, b_stride);
     }
     const u16* at = As[cur];
     const u16* bt = Bs[cur];
@@ -187,6 +196,23 @@ __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restri
   }
 
   // epilogue: lane holds rows 8*(e/4) + 4h + e%4 of each 32x32 tile, column n32
+  if (PARTIAL) {
+    // this slice's float32 tile, element (slice, bz, row, col) of a dense [slice][batch][M][N]
+    float* wbase = ws + (slice * s.batch + bz) * s.M * s.N;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int64_t col = n0 + wn * (BN / 2) + j * 32 + n32;
+        if (col >= s.N) continue;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int64_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (row < s.M) wbase[row * s.N + col] = acc[i][j][e];
+        }
+      }
+    return;
+  }
   u16* cbase = c + bz * s.c_batch;
 #pragma unroll
   for (int i = 0; i < TM; i++)
@@ -206,36 +232,62 @@ __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restri
     }
 }
 
-template <typename T, int BM, int BN, bool A_K, bool B_K>
-int launch_tile(const void* a, const void* b, void* c, const MatmulShape& s, int epilogue, hipStream_t stream) {
-  const int64_t blocks = s.batch * ((s.M + BM - 1) / BM) * ((s.N + BN - 1) / BN);
+// The slices of a split contraction, added per element in slice order, then the epilogue and the
+// store at c's strides.
+template <typename T, int EPI>
+__global__ __launch_bounds__(256) void matmul_splits(const float* __restrict__ ws, u16* __restrict__ c, MatmulShape s,
+                                                     int64_t split) {
+  const int64_t total = s.batch * s.M * s.N;
+  for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    float v = ws[i];
+    for (int64_t k = 1; k < split; k++) v += ws[k * total + i];
+    if (EPI == MATMUL_EPILOGUE_RELU) v = v > 0.f ? v : 0.f;
+    const int64_t col = i % s.N, row = (i / s.N) % s.M, bz = i / (s.N * s.M);
+    c[bz * s.c_batch + row * s.c_m + col * s.c_n] = T::pack(v);
+  }
+}
+
+template <typename T, int BM, int BN, bool A_K, bool B_K, int EPI>
+int launch_tile(const void* a, const void* b, void* c, const MatmulShape& s, const MatmulPlan& plan, void* ws,
+                hipStream_t stream) {
+  const int64_t blocks = plan.split * s.batch * ((s.M + BM - 1) / BM) * ((s.N + BN - 1) / BN);
   if (blocks > 0x7fffffff) return fail(LIMN_HIP_EUNSUPPORTED, "matmul: %lld workgroups exceed one launch", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(MM_THREADS);
-  if (epilogue == MATMUL_EPILOGUE_RELU)
-    hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, MATMUL_EPILOGUE_RELU>), grid, block, 0, stream,
-                       (const u16*)a, (const u16*)b, (u16*)c, s);
-  else
-    hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, MATMUL_EPILOGUE_NONE>), grid, block, 0, stream,
-                       (const u16*)a, (const u16*)b, (u16*)c, s);
-  return check_hip(hipGetLastError(), "launching the matmul kernel");
+  if (plan.split == 1) {
+    hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, false>), grid, block, 0, stream, (const u16*)a,
+                       (const u16*)b, (u16*)c, (float*)nullptr, s, plan.chunk);
+    return check_hip(hipGetLastError(), "launching the matmul kernel");
+  }
+  hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, true>), grid, block, 0, stream, (const u16*)a,
+                     (const u16*)b, (u16*)c, (float*)ws, s, plan.chunk);
+  const int rc = check_hip(hipGetLastError(), "launching the split matmul kernel");
+  if (rc != LIMN_HIP_OK) return rc;
+  const int64_t total = s.batch * s.M * s.N;
+  const int64_t fold_blocks = (total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096;
+  hipLaunchKernelGGL((matmul_splits<T, EPI>), dim3((unsigned)fold_blocks), dim3(256), 0, stream, (const float*)ws,
+                     (u16*)c, s, plan.split);
+  return check_hip(hipGetLastError(), "launching the matmul slice fold");
 }
 
-// 256 x 256 tiles when they still give every compute unit a workgroup, else 128 x 128.
-template <typename T, bool A_K, bool B_K>
-int launch_layout(const void* a, const void* b, void* c, const MatmulShape& s, int epilogue, hipStream_t stream) {
-  const int64_t big = s.batch * ((s.M + 255) / 256) * ((s.N + 255) / 256);
-  if (big >= 256) return launch_tile<T, 256, 256, A_K, B_K>(a, b, c, s, epilogue, stream);
-  return launch_tile<T, 128, 128, A_K, B_K>(a, b, c, s, epilogue, stream);
+template <typename T, bool A_K, bool B_K, int EPI>
+int launch_layout(const void* a, const void* b, void* c, const MatmulShape& s, const MatmulPlan& plan, void* ws,
+                  hipStream_t stream) {
+  if (plan.tile == 256) return launch_tile<T, 256, 256, A_K, B_K, EPI>(a, b, c, s, plan, ws, stream);
+  return launch_tile<T, 128, 128, A_K, B_K, EPI>(a, b, c, s, plan, ws, stream);
 }
 
-template <typename T>
-int launch_type(const void* a, const void* b, void* c, const MatmulShape& s, int epilogue, hipStream_t stream) {
+template <typename T, int EPI>
+int launch_type(const void* a, const void* b, void* c, const MatmulShape& s, const MatmulPlan& plan, void* ws,
+                hipStream_t stream) {
   const bool a_k = s.a_k == 1, b_k = s.b_k == 1;
-  if (a_k && b_k) return launch_layout<T, true, true>(a, b, c, s, epilogue, stream);
-  if (a_k) return launch_layout<T, true, false>(a, b, c, s, epilogue, stream);
-  if (b_k) return launch_layout<T, false, true>(a, b, c, s, epilogue, stream);
-  return launch_layout<T, false, false>(a, b, c, s, epilogue, stream);
+  if (a_k && b_k) return launch_layout<T, true, true, EPI>(a, b, c, s, plan, ws, stream);
+  if (a_k) return launch_layout<T, true, false, EPI>(a, b, c, s, plan, ws, stream);
+  if (b_k) return launch_layout<T, false, true, EPI>(a, b, c, s, plan, ws, stream);
+  return launch_layout<T, false, false, EPI>(a, b, c, s, plan, ws, stream);
 }
+
+constexpr int64_t FILL = 256;        // workgroups that give every CU one (one workgroup per CU fits)
+constexpr int64_t MIN_SLICE = 512;   // shortest k slice worth its partial tile's round trip
 
 }  // namespace
 
@@ -249,9 +301,43 @@ int matmul_layout_ok(const MatmulShape& s) {
   return a_ok && b_ok && batch_ok;
 }
 
-int launch_matmul(const void* a, const void* b, void* c, int dtype, const MatmulShape& s, int epilogue, hipStream_t stream) {
-  if (dtype == LIMN_HIP_BFLOAT16) return launch_type<BF16>(a, b, c, s, epilogue, stream);
-  return launch_type<F16>(a, b, c, s, epilogue, stream);
+// 256 x 256 tiles when they alone give every CU a workgroup; else 128 x 128 tiles when those
+// do; else k is split, into the fewest slices (each at least MIN_SLICE long, a multiple of BK)
+// that fill the machine, on 256 x 256 tiles if the slices can fill it that way, else 128 x 128.
+MatmulPlan plan_matmul(const MatmulShape& s) {
+  const int64_t t256 = s.batch * ((s.M + 255) / 256) * ((s.N + 255) / 256);
+  const int64_t t128 = s.batch * ((s.M + 127) / 128) * ((s.N + 127) / 128);
+  if (t256 >= FILL) return {256, 1, s.K};
+  if (t128 >= FILL || s.K < 2 * MIN_SLICE) return {128, 1, s.K};
+  const int64_t most = s.K / MIN_SLICE;
+  auto cut = [&](int tile, int64_t tiles) -> MatmulPlan {
+    int64_t split = (FILL + tiles - 1) / tiles;
+    split = split < most ? split : most;
+    int64_t chunk = (s.K + split - 1) / split;
+    chunk = (chunk + BK - 1) / BK * BK;
+    return {tile, (s.K + chunk - 1) / chunk, chunk};
+  };
+  const MatmulPlan big = cut(256, t256);
+  if (big.split * t256 >= FILL) return big;
+  return cut(128, t128);
+}
+
+int64_t matmul_workspace_bytes(const MatmulShape& s) {
+  const MatmulPlan plan = plan_matmul(s);
+  return plan.split > 1 ? plan.split * s.batch * s.M * s.N * (int64_t)sizeof(float) : 0;
+}
+
+int launch_matmul(const void* a, const void* b, void* c, int dtype, const MatmulShape& s, int epilogue, void* workspace,
+                  int64_t workspace_bytes, hipStream_t stream) {
+  MatmulPlan plan = plan_matmul(s);
+  if (plan.split > 1 && (workspace == nullptr || workspace_bytes < matmul_workspace_bytes(s)))
+    plan = {plan.tile, 1, s.K};  // no room for the slices: the same contraction, unsplit
+  const bool relu = epilogue == MATMUL_EPILOGUE_RELU;
+  if (dtype == LIMN_HIP_BFLOAT16)
+    return relu ? launch_type<BF16, MATMUL_EPILOGUE_RELU>(a, b, c, s, plan, workspace, stream)
+                : launch_type<BF16, MATMUL_EPILOGUE_NONE>(a, b, c, s, plan, workspace, stream);
+  return relu ? launch_type<F16, MATMUL_EPILOGUE_RELU>(a, b, c, s, plan, workspace, stream)
+              : launch_type<F16, MATMUL_EPILOGUE_NONE>(a, b, c, s, plan, workspace, stream);
 }
 
 }  // namespace limn

@@ -499,9 +499,13 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     # can put a row index innermost merely because small per-row vectors are stride-1 along it.
     along = stride_one_var(nest, shape)
     columns = along is not None and along not in {v for v, _ in shape.inner}
+    if columns:
+        # cells are consecutive along the stride-1 var: decode it fastest
+        shape.outer = [o for o in shape.outer if o[0] != along] + [o for o in shape.outer if o[0] == along]
+    if columns and R >= 64 and cells < (1 << 18):
+        return plan_columns(nest, shape, bufs, cells, R)
     if columns and cells >= 1024:
         group = 1
-        shape.outer = [o for o in shape.outer if o[0] != along] + [o for o in shape.outer if o[0] == along]
     elif R < 64 or (cells >= (1 << 20) and R <= 256):
         group = 1
     elif R < 4096:
@@ -611,6 +615,75 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     return Planned(source, launches, scratch_bytes=cells * parts * acc_dt.itemsize, notes={"parts": parts, "vec": vec})
 
 
+COLUMN_TILE = 64  # cells per workgroup of a column reduce: one wave's lanes, one coalesced row piece
+COLUMN_BLOCKS = 2048  # workgroups a column reduce aims for (8 per CU): tiles x row parts
+
+
+def plan_columns(nest: LoopNest, shape: NestShape, bufs: Buffers, cells: int, R: int) -> Planned:
+    """A reduce whose cells run along the stride-1 var and whose reduce vars are strided (a bias
+    or LayerNorm-parameter gradient: a sum over every (batch, time) row of a (.., C) tensor).
+    A workgroup takes 64 consecutive cells, one per lane, so each row it reads is one coalesced
+    piece; its 4 waves take interleaved rows of one part of the reduce range; the parts, as many
+    as fill the machine, are partial totals in scratch folded per cell in order by a second
+    kernel (one part: written directly). Totals are deterministic."""
+    rdt = shape.reduce_dtype
+    acc_dt = accumulate_in(rdt)
+    acc_t = VALUE_T[acc_dt]
+    out_dtype = nest.kernel.target.dtype
+    wide = bufs.wide_index or cells * R > (1 << 30)
+    ident = literal(shape.identity, acc_dt)
+    fold = shape.fold
+    waves = THREADS // 64
+    tiles = -(-cells // COLUMN_TILE)
+    parts = max(1, min(-(-COLUMN_BLOCKS // tiles), R // (4 * waves)))
+    per_part = -(-R // parts)
+    out_ref = f"out[{render_index(shape.out_index, wide)}]"
+    body = ["      " + value_line(i, bufs) for i in shape.body]
+    name = nest.name if parts == 1 else nest.name + "_part"
+    params = [f"const {STORE_T[n.dtype]}* __restrict__ in{k}" for k, n in enumerate(nest.kernel.inputs)]
+    params.append(f"{STORE_T[out_dtype]}* __restrict__ out" if parts == 1 else f"{acc_t}* __restrict__ scratch")
+    lines = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}({", ".join(params)}) {{']
+    lines.append("  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;")
+    lines.append(f"  const i64 tile = blockIdx.x / {parts}, p_ = blockIdx.x % {parts};")
+    lines.append(f"  const i64 g = tile * {COLUMN_TILE} + lane;")
+    lines.append(f"  {acc_t} acc = {ident};")
+    lines.append(f"  if (g < {cells}LL) {{")
+    lines += decode(shape.outer, "g", "    ", wide)
+    lines.append(f"    const i64 stop_ = (p_ + 1) * {per_part}LL < {R}LL ? (p_ + 1) * {per_part}LL : {R}LL;")
+    lines.append(f"    for (i64 r_ = p_ * {per_part}LL + wave; r_ < stop_; r_ += {waves}) {{")
+    lines += decode(shape.inner, "r_", "      ", True)
+    lines += body
+    lines.append("      " + _fold(fold, "acc", f"({acc_t}){shape.item}"))
+    lines += ["    }", "  }"]
+    # the waves' totals for each lane's cell, folded in wave order
+    lines.append(f"  __shared__ {acc_t} lds_[{waves}][64];")
+    lines.append("  lds_[wave][lane] = acc;")
+    lines.append("  __syncthreads();")
+    lines.append(f"  if (wave == 0 && g < {cells}LL) {{")
+    lines.append("    acc = lds_[0][lane];")
+    for w in range(1, waves):
+        lines.append("    " + _fold(fold, "acc", f"lds_[{w}][lane]"))
+    if parts == 1:
+        lines += decode(shape.outer, "g", "    ", wide)
+        lines.append(f"    {out_ref} = {store_expr(out_dtype, 'acc')};")
+    else:
+        lines.append(f"    scratch[p_ * {cells}LL + g] = acc;  // [part][cell]: the final fold reads rows")
+    lines += ["  }", "}"]
+    launches = [Launch(name, tiles * parts, THREADS, "io" if parts == 1 else "io_scratch")]
+    if parts == 1:
+        return Planned("\n".join(lines), launches, notes={"columns": True, "parts": 1})
+    final = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {nest.name}(const {acc_t}* __restrict__ scratch, {STORE_T[out_dtype]}* __restrict__ out) {{']
+    final.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {cells}LL; g += (i64)gridDim.x * {THREADS}) {{")
+    final += decode(shape.outer, "g", "    ", wide)
+    final.append(f"    {acc_t} acc = scratch[g];")
+    final.append(f"    for (int p_ = 1; p_ < {parts}; p_++) " + _fold(fold, "acc", f"scratch[p_ * {cells}LL + g]"))
+    final.append(f"    {out_ref} = {store_expr(out_dtype, 'acc')};")
+    final += ["  }", "}"]
+    launches.append(Launch(nest.name, max(1, min(-(-cells // THREADS), 1 << 20)), THREADS, "scratch_out"))
+    return Planned("\n".join(lines) + "\n" + "\n".join(final), launches, scratch_bytes=cells * parts * acc_dt.itemsize,
+                   notes={"columns": True, "parts": parts})
+
+
 def plan_nest(nest: LoopNest) -> Planned:
     kernel = nest.kernel
     dtypes = {f"in{k}": n.dtype for k, n in enumerate(kernel.inputs)}
@@ -666,12 +739,17 @@ def _contraction_runner(dev, con: Contraction):
     lib = dev.lib
     code = ABI_CODE[con.dtype]
     size = con.dtype.itemsize
-    tail = (code, con.batch, con.M, con.N, con.K, con.a_batch, con.a_m, con.a_k, con.b_batch, con.b_k, con.b_n, con.c_batch, con.c_m, con.c_n, 0, None)
+    shape = (code, con.batch, con.M, con.N, con.K, con.a_batch, con.a_m, con.a_k, con.b_batch, con.b_k, con.b_n, con.c_batch, con.c_m, con.c_n, 0)
+    ws_bytes = int(lib.limn_hip_matmul_workspace(code, con.batch, con.M, con.N, con.K))
+    held: list = []  # the split-k workspace, allocated on first use and kept with the runner
 
     def run(inputs: list, outs: list) -> None:
+        if ws_bytes and not held:
+            held.append(dev._alloc(ws_bytes))
         a = inputs[con.a_input].ptr + con.a_offset * size
         b = inputs[con.b_input].ptr + con.b_offset * size
-        runtime.check_limn(lib.limn_hip_matmul(a, b, outs[0].ptr, *tail))
+        ws = held[0].ptr if held else None
+        runtime.check_limn(lib.limn_hip_matmul(a, b, outs[0].ptr, *shape, ws, ws_bytes, None))
 
     return run
 

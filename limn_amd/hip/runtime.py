@@ -27,6 +27,7 @@ P = ctypes.POINTER
 c_int64 = ctypes.c_int64
 
 ARCH = "gfx950"
+ABI_VERSION = 2  # LIMN_HIP_ABI_VERSION of include/limn_hip.h
 LIBRARY = Path(__file__).resolve().parent.parent / "liblimn_hip.so"
 
 # hipMemcpyKind
@@ -76,7 +77,8 @@ _LIMN = {
     "limn_hip_last_error": (c_char_p, []),
     "limn_hip_device_info": (c_int, [c_int, c_char_p, c_int, P(c_int), P(c_int), P(c_int64)]),
     "limn_hip_sdpa_path": (c_int, [c_int, _I64, _I64]),
-    "limn_hip_matmul": (c_int, [c_void_p, c_void_p, c_void_p, c_int] + [_I64] * 13 + [c_int, c_void_p]),
+    "limn_hip_matmul": (c_int, [c_void_p, c_void_p, c_void_p, c_int] + [_I64] * 13 + [c_int, c_void_p, _I64, c_void_p]),
+    "limn_hip_matmul_workspace": (_I64, [c_int, _I64, _I64, _I64, _I64]),
     "limn_hip_matmul_supported": (c_int, [c_int] + [_I64] * 9),
     "limn_hip_sdpa_fwd": (
         c_int,
@@ -133,8 +135,8 @@ def kernels() -> ctypes.CDLL:
     if not LIBRARY.exists():
         raise RuntimeError(f"{LIBRARY} is missing: build it with `python -m limn_amd.build` (hipcc, gfx950)")
     lib = _bind(ctypes.CDLL(str(LIBRARY)), _LIMN)
-    if lib.limn_hip_abi_version() != 1:
-        raise RuntimeError(f"{LIBRARY} speaks ABI {lib.limn_hip_abi_version()}, this package expects 1: rebuild it")
+    if lib.limn_hip_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{LIBRARY} speaks ABI {lib.limn_hip_abi_version()}, this package expects {ABI_VERSION}: rebuild it")
     return lib
 
 

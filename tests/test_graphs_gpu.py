@@ -343,3 +343,72 @@ def test_config3_full_size(hipdev):
     got = out.numpy()
     want = bf16_values(bf16_bits(np.maximum(a_vals @ b_vals, 0.0)))
     np.testing.assert_allclose(got, want, rtol=2e-2, atol=2e-2)
+
+
+def test_weight_gradient_is_one_split_k_contraction(hipdev):
+    """A weight gradient sums over batch and rows together (K = 8 * 512 = 4096) into a 256 x 128
+    output: one contraction, split in k (the output is two 128-tiles), its slices added in order.
+    Checked against the float64 closed form on the same bf16 values and the float32 total rounded
+    once at the store."""
+    from limn_amd.dtypes import bf16_bits, bf16_values
+    from limn_amd.hip import runtime
+
+    B, T, C, O = 8, 512, 128, 256
+    x_vals = bf16_values(bf16_bits(rng.standard_normal((B, T, C)).astype(np.float32)))
+    dy_vals = bf16_values(bf16_bits(rng.standard_normal((B, T, O)).astype(np.float32)))
+    limn_device.active_device = hipdev
+    x, dy = Tensor(x_vals, dtype=bfloat16), Tensor(dy_vals, dtype=bfloat16)
+    w = Tensor(np.zeros((O, C), np.float32), requires_grad=True)
+    (gw,) = grad((x @ w.cast(bfloat16).transpose() * dy).sum(), [w])
+    plans = _plans(hipdev, gw)
+    cons = [p.contraction for p in plans if p.contraction is not None]
+    wgrad = [c for c in cons if c.K == B * T]
+    assert wgrad, f"no contraction over batch and rows: {[(c.M, c.N, c.K) for c in cons]}"
+    c = wgrad[0]
+    assert runtime.kernels().limn_hip_matmul_workspace(3, c.batch, c.M, c.N, c.K) > 0, "this shape should split k"
+    got = gw.numpy().astype(np.float64)
+    exact = np.einsum("bto,btc->oc", dy_vals.astype(np.float64), x_vals.astype(np.float64))
+    np.testing.assert_allclose(got, exact, rtol=2**-7, atol=1e-2)
+
+
+def test_split_k_without_workspace_runs_unsplit(hipdev):
+    """The C ABI with no workspace for a shape that wants one: the same contraction, unsplit."""
+    from limn_amd.dtypes import bf16_bits, bf16_values
+    from limn_amd.hip import runtime
+
+    M, N, K = 256, 128, 4096  # c[m, n] = sum_k a[m, k] b[k, n], a m-contiguous, b n-contiguous
+    a_vals = bf16_values(bf16_bits(rng.standard_normal((K, M)).astype(np.float32)))
+    b_vals = bf16_values(bf16_bits(rng.standard_normal((K, N)).astype(np.float32)))
+    lib = runtime.kernels()
+    ws_bytes = lib.limn_hip_matmul_workspace(3, 1, M, N, K)
+    assert ws_bytes > 0
+    a, b = hipdev.alloc(a_vals.size * 2), hipdev.alloc(b_vals.size * 2)
+    hipdev.copyin(a, bf16_bits(a_vals))
+    hipdev.copyin(b, bf16_bits(b_vals))
+    outs = []
+    for ws in (None, hipdev.alloc(ws_bytes)):
+        c = hipdev.alloc(M * N * 2)
+        runtime.check_limn(lib.limn_hip_matmul(a.ptr, b.ptr, c.ptr, 3, 1, M, N, K, 0, 1, M, 0, N, 1, 0, N, 1, 0,
+                                               None if ws is None else ws.ptr, 0 if ws is None else ws_bytes, None))
+        hipdev.finish()
+        outs.append(bf16_values(hipdev.copyout(c).view(np.uint16).reshape(M, N)).astype(np.float64))
+    exact = a_vals.astype(np.float64).T @ b_vals.astype(np.float64)
+    for got in outs:
+        np.testing.assert_allclose(got, exact, rtol=2**-7, atol=1e-2)
+
+
+@pytest.mark.parametrize("shape,dtype", [((8, 512, 96), float32), ((4, 300, 1536), bfloat16), ((2, 64, 200), float32)], ids=str)
+def test_column_reduce_over_batch_and_rows(hipdev, shape, dtype):
+    """A bias gradient's shape: (b, t, c) summed over b and t. 64 cells per workgroup, rows
+    split into parts; a partial last tile (c % 64) and a single-part case (few rows) included."""
+    x = Tensor(rng.standard_normal(shape).astype(np.float32), dtype=dtype)
+    tol = 1e-4 if dtype is float32 else 2e-2
+    check(hipdev, x.sum(axis=(0, 1)), rtol=tol, atol=tol)
+    check(hipdev, (x * x).sum(axis=(0, 1), keepdim=True), rtol=tol, atol=tol)
+
+
+def test_column_max_keeps_nan(hipdev):
+    x = rng.standard_normal((16, 128, 70)).astype(np.float32)
+    x[3, 17, 5] = np.nan
+    x[9, 100, 69] = np.nan
+    check(hipdev, Tensor(x).max(axis=(0, 1)))
