@@ -6,6 +6,9 @@ embeddings; a final LayerNorm and an unbiased head) at the size the C5 configura
 vocab 256, d_model 512, 8 layers, 8 heads (head dim 64), context 512, batch 32, MLP with tanh
 GELU, AdamW (lr 3e-4, weight decay 0.1).
 
+The residual stream (and its gradient) is materialized after every sublayer; see
+`materialized`.
+
 Mixed precision, explicit in the graph: parameters (and AdamW's state) stay float32 masters;
 each Linear casts its weight and bias to the activation dtype at use, so the products run as
 bf16 contractions with float32 totals; LayerNorm statistics and the loss's log-softmax are
@@ -21,7 +24,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from limn_amd.nn import Embedding, LayerNorm, Linear, gelu, parameters
-from limn_amd.ops import DType, bfloat16, float32, int32
+from limn_amd.ops import DType, Node, Op, bfloat16, float32, int32
 from limn_amd.optim import AdamW
 from limn_amd.tensor import Tensor
 
@@ -51,6 +54,14 @@ class GPTConfig:
         return 6.0 * self.matmul_params() + self.layers * 3 * 4 * self.ctx * self.dim / 2
 
 
+def materialized(x: Tensor) -> Tensor:
+    """x written to memory once (a CONTIGUOUS node, a scheduler cut), and in the backward its
+    gradient too. The residual stream is read by every later sublayer: left as an expression, the
+    scheduler fuses the whole sum into each reader, which then re-reads every term ever added to
+    it (traffic quadratic in depth, in the forward and again in the backward)."""
+    return Tensor.from_node(Node(Op.CONTIGUOUS, (x.node,), x.dtype, x.shape), (x,), lambda g: (materialized(g),))
+
+
 def mixed(layer: Linear, x: Tensor) -> Tensor:
     """A Linear with its float32 weight and bias cast to x's dtype at use."""
     y = x @ layer.weight.cast(x.dtype).transpose()
@@ -76,8 +87,8 @@ class Block:
         hd = c // self.heads
         q, k, v = mixed(self.qkv, normed(self.ln1, x)).reshape(b, t, 3, self.heads, hd).permute(2, 0, 3, 1, 4)
         att = q.attention(k, v, causal=True)
-        x = x + mixed(self.proj, att.permute(0, 2, 1, 3).reshape(b, t, c))
-        return x + mixed(self.down, gelu(mixed(self.up, normed(self.ln2, x))))
+        x = materialized(x + mixed(self.proj, att.permute(0, 2, 1, 3).reshape(b, t, c)))
+        return materialized(x + mixed(self.down, gelu(mixed(self.up, normed(self.ln2, x)))))
 
 
 class GPT:
@@ -90,7 +101,7 @@ class GPT:
         self.head = Linear(cfg.dim, cfg.vocab, bias=False)
 
     def __call__(self, tokens: Tensor) -> Tensor:
-        x = (self.tok(tokens) + self.pos(Tensor.arange(self.cfg.ctx))).cast(self.cfg.dtype)
+        x = materialized((self.tok(tokens) + self.pos(Tensor.arange(self.cfg.ctx))).cast(self.cfg.dtype))
         for block in self.blocks:
             x = block(x)
         return mixed(self.head, normed(self.ln, x))
