@@ -364,7 +364,7 @@ def bench_c3(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
             "peak": MFMA_BF16_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": round(flops / (mm * 1e-3) / MFMA_BF16_PEAK, 4),
-            "traffic": traffic("c3:matmul_mfma<BF16,256,256,true,false,0>"),
+            "traffic": traffic("c3:matmul_mfma<BF16,256,256,true,false,0,false>"),
         },
         "cpu_baseline": None if cpu_s is None else {
             "value": round(2.0 * rows * n * n / cpu_s / 1e12, 6),
@@ -630,7 +630,7 @@ def main() -> int:
     # the template instance each CUSTOM name runs at this configuration (rocprofv3's kernel names)
     KERNEL_SYMBOL = {
         "sdpa": "sdpa_fwd_mfma<BF16,128,1,true,false>",
-        "sdpa_bwd_q": "sdpa_bwd_q_mfma<BF16,128,2,true,false>",
+        "sdpa_bwd_q": "sdpa_bwd_q_mfma<BF16,128,1,true,false>",
         "sdpa_bwd_kv": "sdpa_bwd_kv_mfma<BF16,128,1,true,false>",
     }
     dom = int(np.argmax(per))
