@@ -19,12 +19,11 @@
 // slices per element in slice order, applies the epilogue and rounds, so the result does not
 // depend on scheduling.
 //
-// LDS holds both operands k-contiguous (A as [m][k], B as [n][k], rows padded by 8 elements
-// so 16-byte reads across a 32-row operand are conflict-free), so each MFMA operand is one
-// ds_read_b128. An operand that is k-contiguous in memory is staged with 16-byte row loads;
-// one that is m- (or n-) contiguous is loaded 4 k-rows x 8 columns per thread and transposed
-// in registers on the way into LDS, its k positions rotated per 16-row group so that those
-// transposed writes spread over the banks.
+// LDS holds each operand in its memory orientation, copied with 16-byte loads through a buffer
+// resource (rows and k past the operand's end read as zeros, so the loop has no bounds tests). A
+// k-contiguous operand's tile is [rows][64 + 8] and each MFMA operand is one ds_read_b128 of a
+// row; an m- (or n-) contiguous operand's tile is [64][rows + 32] and each MFMA operand is two
+// transposing ds_read_b64_tr_b16. The paddings make every LDS read and write conflict-free.
 
 #include "matmul.h"
 
@@ -33,103 +32,89 @@ namespace {
 
 constexpr int MM_THREADS = 256;
 constexpr int BK = 64;
-constexpr int LS = BK + 8;  // LDS row stride (elements) of both operand tiles
 
 __device__ __forceinline__ u16x8 zero8() {
   u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
   return z;
 }
 
-// k position of element k in LDS row `row` of an operand staged from row-contiguous memory:
-// rotated by 8 per 16-row group (identity for k-contiguous staging). gfx950's LDS has 64
-// four-byte banks and serves 16 lanes of a 16-byte read (32 lanes of an 8-byte write) per cycle.
-// The row stride LS is 36 banks, so an operand read (16 consecutive rows, one rotation) starts
-// in 16 distinct 4-bank groups; a staging write (rows 8 apart) would land every even and every
-// odd row on one group, and the rotation by row >> 4 spreads them over all 16. Together with
-// the lane-to-block map of OperandStage (k groups of opposite parity, 8 bytes apart, in the
-// two 16-lane halves) the 32 lanes of a write fill all 64 banks.
-template <bool KCONTIG>
-__device__ __forceinline__ int kpos(int row, int k) {
-  return KCONTIG ? k : ((k + 8 * ((row >> 4) & 7)) & (BK - 1));
-}
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
-// Block `blk` of a row-contiguous operand stage -> (8-row chunk rc, 4-deep k group kg): lanes
-// 0-15 take 16 consecutive row chunks with an even k group, lanes 16-31 the same chunks with the
-// next (odd) one; loads stay 256-byte coalesced per k row.
-template <int ROWS>
-__device__ __forceinline__ void stage_block(int blk, int& rc, int& kg) {
-  constexpr int R16 = ROWS / 128;  // 16-chunk groups of rows
-  rc = (blk & 15) | (((blk >> 5) % R16) << 4);
-  kg = ((blk >> 4) & 1) | (((blk >> 5) / R16) << 1);
-}
-
-// One operand's stage: ROWS (m or n) x BK values, staged into an LDS tile [row][k].
-//   KCONTIG: memory is k-contiguous: element (row, k) at base + row*stride + k.
-//   else   : memory is row-contiguous: element (row, k) at base + k*stride + row.
+// One operand's LDS tile per stage, kept in its memory orientation:
+//   k-contiguous operand -> [ROWS][BK + 8]: an MFMA operand is one ds_read_b128 of a row (the
+//     row stride is 9 sixteen-byte groups, so the 16 rows a read serves per cycle hit 16 groups);
+//   row-contiguous operand -> [BK][ROWS + 32]: an MFMA operand is two transposing
+//     ds_read_b64_tr_b16 (a stride of 256 + 64 bytes puts the 4 k rows a 32-lane half reads into
+//     4 different quarters of the 64 banks).
+// Staging is plain 16-byte copies (8 consecutive lanes write 128 contiguous bytes): nothing is
+// transposed in registers.
 template <int ROWS, bool KCONTIG>
-struct OperandStage {
-  static constexpr int LOADS = ROWS * BK / 8 / MM_THREADS;  // 16-byte loads per thread
+struct Operand {
+  static constexpr int STRIDE = KCONTIG ? BK + 8 : ROWS + 32;
+  static constexpr int ELEMS = STRIDE * (KCONTIG ? ROWS : BK);
+  static constexpr int PER_ROW = KCONTIG ? BK / 8 : ROWS / 8;  // 16-byte chunks per LDS row
+  static constexpr int LOADS = ROWS * BK / 8 / MM_THREADS;      // chunks per thread per stage
+  __amdgpu_buffer_rsrc_t rsrc;
+  int stride, row0;
   u16x8 r[LOADS];
 
-  __device__ __forceinline__ void load(const u16* base, int64_t row0, int64_t rows, int64_t k0, int64_t depth,
-                                       int64_t stride) {
-    if (KCONTIG) {
+  // base: the operand's batch slice; `rows` (m or n) and `depth` (k) bound the bytes the
+  // resource covers, so rows or k beyond them read as zeros without a test
+  __device__ __forceinline__ Operand(const u16* base, int64_t rows, int64_t depth, int64_t stride_, int64_t row0_) {
+    stride = (int)stride_;
+    row0 = (int)row0_;
+    const int64_t extent = KCONTIG ? (rows - 1) * stride_ + depth : (depth - 1) * stride_ + rows;
+    rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(extent * 2), 0x00020000);
+  }
+
+  // the stage starting at k0; chunks at or past `depth` are zeroed when TAIL (a k-contiguous row
+  // runs on into the next row's elements there)
+  template <bool TAIL>
+  __device__ __forceinline__ void load(int k0, int depth) {
 #pragma unroll
-      for (int s = 0; s < LOADS; s++) {
-        const int c = threadIdx.x + s * MM_THREADS;
-        const int row = c / (BK / 8), kc = c % (BK / 8);
-        const int64_t gr = row0 + row, gk = k0 + kc * 8;
-        r[s] = (gr < rows && gk < depth) ? *(const u16x8*)(base + gr * stride + gk) : zero8();
-      }
-    } else {
-      // a block is 4 k-rows x 8 columns; column chunks vary fastest across lanes (coalesced)
-#pragma unroll
-      for (int s = 0; s < LOADS / 4; s++) {
-        const int blk = threadIdx.x + s * MM_THREADS;
-        int rc, kg;
-        stage_block<ROWS>(blk, rc, kg);
-        const int64_t gr = row0 + rc * 8;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int64_t gk = k0 + kg * 4 + e;
-          r[4 * s + e] = (gr < rows && gk < depth) ? *(const u16x8*)(base + gk * stride + gr) : zero8();
-        }
-      }
+    for (int s = 0; s < LOADS; s++) {
+      const int c = threadIdx.x + s * MM_THREADS;
+      const int lrow = c / PER_ROW, lcol = (c % PER_ROW) * 8;
+      const int off = KCONTIG ? (row0 + lrow) * stride + k0 + lcol : (k0 + lrow) * stride + row0 + lcol;
+      r[s] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off * 2, 0, 0));
+      if (TAIL && KCONTIG && k0 + lcol >= depth) r[s] = zero8();
     }
   }
 
-  __device__ __forceinline__ void store(u16* lds) {
-    if (KCONTIG) {
+  __device__ __forceinline__ void store(u16* lds) const {
 #pragma unroll
-      for (int s = 0; s < LOADS; s++) {
-        const int c = threadIdx.x + s * MM_THREADS;
-        const int row = c / (BK / 8), kc = c % (BK / 8);
-        *(u16x8*)(lds + row * LS + kc * 8) = r[s];
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < LOADS / 4; s++) {
-        const int blk = threadIdx.x + s * MM_THREADS;
-        int rc, kg;
-        stage_block<ROWS>(blk, rc, kg);
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-          u16x4 t = {r[4 * s][c], r[4 * s + 1][c], r[4 * s + 2][c], r[4 * s + 3][c]};
-          const int row = rc * 8 + c;
-          *(u16x4*)(lds + row * LS + kpos<false>(row, kg * 4)) = t;
-        }
-      }
+    for (int s = 0; s < LOADS; s++) {
+      const int c = threadIdx.x + s * MM_THREADS;
+      *(u16x8*)(lds + (c / PER_ROW) * STRIDE + (c % PER_ROW) * 8) = r[s];
     }
+  }
+
+  // the MFMA operand of the 32 rows at `row` for the 16-deep k step kk: lane l gets
+  // X[row + l % 32][16 kk + 8 (l / 32) + j], j = 0..7
+  __device__ __forceinline__ u16x8 operand(const u16* lds, int row, int kk) const {
+    const int lane = threadIdx.x & 63;
+    if (KCONTIG) return *(const u16x8*)(lds + (row + (lane & 31)) * STRIDE + kk * 16 + 8 * (lane >> 5));
+    // within each 16-lane group, lane i's item j' comes from the 8 bytes lane 4j' + i/4
+    // addresses, element i % 4: lane r addresses k row 16kk + 8(l/32) + 4 inst + r/4, columns
+    // row + 16((l/16) % 2) + 4(r % 4)
+    const int g = lane >> 4, i = lane & 15;
+    u16* p = (u16*)lds + (kk * 16 + 8 * (g >> 1) + (i >> 2)) * STRIDE + row + 16 * (g & 1) + 4 * (i & 3);
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)p);
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + 4 * STRIDE));
+    return __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   }
 };
 
-template <typename T, int BM, int BN, bool A_K, bool B_K, int EPI, bool PARTIAL>
+template <typename T, int BM, int BN, bool A_K, bool B_K, int EPI, bool PARTIAL, bool TAIL>
 __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restrict__ a, const u16* __restrict__ b,
                                                              u16* __restrict__ c, float* __restrict__ ws, MatmulShape s,
                                                              int64_t chunk) {
   constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 accumulators per wave along m and n
-  __shared__ __attribute__((aligned(16))) u16 As[2][BM * LS];
-  __shared__ __attribute__((aligned(16))) u16 Bs[2][BN * LS];
+  using OA = Operand<BM, A_K>;
+  using OB = Operand<BN, B_K>;
+  __shared__ __attribute__((aligned(16))) u16 As[2][OA::ELEMS];
+  __shared__ __attribute__((aligned(16))) u16 Bs[2][OB::ELEMS];
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n32 = lane & 31;
   const int wm = wave >> 1, wn = wave & 1;
@@ -141,8 +126,6 @@ __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restri
   const int64_t k_lo = slice * chunk, k_hi = k_lo + chunk < s.K ? k_lo + chunk : s.K;
   const int64_t tm = t / tiles_n, tn = t - tm * tiles_n;
   const int64_t m0 = tm * BM, n0 = tn * BN;
-  const u16* abase = a + bz * s.a_batch;
-  const u16* bbase = b + bz * s.b_batch;
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -152,46 +135,40 @@ __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restri
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
-  OperandStage<BM, A_K> sa;
-  OperandStage<BN, B_K> sb;
-  const int64_t a_stride = A_K ? s.a_m : s.a_k;
-  const int64_t b_stride = B_K ? s.b_n : s.b_k;
+  OA sa(a + bz * s.a_batch, s.M, s.K, A_K ? s.a_m : s.a_k, m0);
+  OB sb(b + bz * s.b_batch, s.N, s.K, B_K ? s.b_n : s.b_k, n0);
   const int stages = (int)((k_hi - k_lo + BK - 1) / BK);
-  sa.load(abase, m0, s.M, k_lo, k_hi, a_stride);
-  sb.load(bbase, n0, s.N, k_lo, k_hi, b_stride);
+  const int kb = (int)k_lo, depth = (int)k_hi;
+  sa.template load<TAIL>(kb, depth);
+  sb.template load<TAIL>(kb, depth);
   sa.store(As[0]);
   sb.store(Bs[0]);
+  sa.template load<TAIL>(kb + BK, depth);
+  sb.template load<TAIL>(kb + BK, depth);
   __syncthreads();
+  // one basic block per stage: the next stage's stores and the one after's loads are
+  // unconditional (past the last stage they fill the idle buffer, or read zeros), so the compiler
+  // can interleave them with the MFMAs
   for (int st = 0; st < stages; st++) {
     const int cur = st & 1;
-    if (st + 1 < stages) {
-      sa.load(abase, m0, s.M, k_lo + (int64_t)(st + 1) * BK, k_hi, a_stride);
-      sb.load(bbase, n0, s.N, k_lo + (int64_t)(st + 1) * BK, k_hi, b_stride);
-    }
     const u16* at = As[cur];
     const u16* bt = Bs[cur];
 #pragma unroll
     for (int kk = 0; kk < BK / 16; kk++) {
       u16x8 av[TM], bv[TN];
 #pragma unroll
-      for (int i = 0; i < TM; i++) {
-        const int row = wm * (BM / 2) + i * 32 + n32;
-        av[i] = *(const u16x8*)(at + row * LS + kpos<A_K>(row, kk * 16 + 8 * h));
-      }
+      for (int i = 0; i < TM; i++) av[i] = sa.operand(at, wm * (BM / 2) + i * 32, kk);
 #pragma unroll
-      for (int j = 0; j < TN; j++) {
-        const int row = wn * (BN / 2) + j * 32 + n32;
-        bv[j] = *(const u16x8*)(bt + row * LS + kpos<B_K>(row, kk * 16 + 8 * h));
-      }
+      for (int j = 0; j < TN; j++) bv[j] = sb.operand(bt, wn * (BN / 2) + j * 32, kk);
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = T::mfma32(av[i], bv[j], acc[i][j]);
     }
-    if (st + 1 < stages) {
-      sa.store(As[cur ^ 1]);
-      sb.store(Bs[cur ^ 1]);
-    }
+    sa.store(As[cur ^ 1]);
+    sb.store(Bs[cur ^ 1]);
+    sa.template load<TAIL>(kb + (st + 2) * BK, depth);
+    sb.template load<TAIL>(kb + (st + 2) * BK, depth);
     __syncthreads();
   }
 
@@ -253,13 +230,22 @@ int launch_tile(const void* a, const void* b, void* c, const MatmulShape& s, con
   const int64_t blocks = plan.split * s.batch * ((s.M + BM - 1) / BM) * ((s.N + BN - 1) / BN);
   if (blocks > 0x7fffffff) return fail(LIMN_HIP_EUNSUPPORTED, "matmul: %lld workgroups exceed one launch", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(MM_THREADS);
+  const bool tail = (s.K % BK) != 0 || (plan.chunk % BK) != 0;
   if (plan.split == 1) {
-    hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, false>), grid, block, 0, stream, (const u16*)a,
-                       (const u16*)b, (u16*)c, (float*)nullptr, s, plan.chunk);
+    if (tail)
+      hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, false, true>), grid, block, 0, stream, (const u16*)a,
+                         (const u16*)b, (u16*)c, (float*)nullptr, s, plan.chunk);
+    else
+      hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, false, false>), grid, block, 0, stream, (const u16*)a,
+                         (const u16*)b, (u16*)c, (float*)nullptr, s, plan.chunk);
     return check_hip(hipGetLastError(), "launching the matmul kernel");
   }
-  hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, true>), grid, block, 0, stream, (const u16*)a,
-                     (const u16*)b, (u16*)c, (float*)ws, s, plan.chunk);
+  if (tail)
+    hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, true, true>), grid, block, 0, stream, (const u16*)a,
+                       (const u16*)b, (u16*)c, (float*)ws, s, plan.chunk);
+  else
+    hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, true, false>), grid, block, 0, stream, (const u16*)a,
+                       (const u16*)b, (u16*)c, (float*)ws, s, plan.chunk);
   const int rc = check_hip(hipGetLastError(), "launching the split matmul kernel");
   if (rc != LIMN_HIP_OK) return rc;
   const int64_t total = s.batch * s.M * s.N;
@@ -298,7 +284,14 @@ int matmul_layout_ok(const MatmulShape& s) {
   const bool a_ok = (s.a_k == 1 && s.a_m % 8 == 0 && s.K % 8 == 0) || (s.a_m == 1 && s.a_k % 8 == 0 && s.M % 8 == 0);
   const bool b_ok = (s.b_k == 1 && s.b_n % 8 == 0 && s.K % 8 == 0) || (s.b_n == 1 && s.b_k % 8 == 0 && s.N % 8 == 0);
   const bool batch_ok = s.a_batch % 8 == 0 && s.b_batch % 8 == 0;
-  return a_ok && b_ok && batch_ok;
+  // the kernel addresses each operand's batch slice through a buffer resource with 32-bit byte
+  // offsets; a tile overhanging the last row or the last stage by up to 256 rows or 3 stages
+  // must still be addressable
+  auto reach = [](int64_t rows, int64_t depth, int64_t row_stride, int64_t k_stride) {
+    return ((rows + 256) * row_stride + (depth + 3 * BK) * k_stride + 256) * 2;
+  };
+  const bool reach_ok = reach(s.M, s.K, s.a_m, s.a_k) < INT32_MAX && reach(s.N, s.K, s.b_n, s.b_k) < INT32_MAX;
+  return a_ok && b_ok && batch_ok && reach_ok;
 }
 
 // 256 x 256 tiles when they alone give every CU a workgroup; else 128 x 128 tiles when those

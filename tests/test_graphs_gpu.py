@@ -397,6 +397,40 @@ def test_split_k_without_workspace_runs_unsplit(hipdev):
         np.testing.assert_allclose(got, exact, rtol=2**-7, atol=1e-2)
 
 
+@pytest.mark.parametrize("a_kcontig", [True, False], ids=["a-k", "a-m"])
+@pytest.mark.parametrize("b_kcontig", [True, False], ids=["b-k", "b-n"])
+@pytest.mark.parametrize("M,N,K,relu", [(256, 128, 4104, False), (200, 72, 1000, True), (520, 264, 72, False)], ids=str)
+def test_matmul_layouts_through_the_c_abi(hipdev, a_kcontig, b_kcontig, M, N, K, relu):
+    """Every operand orientation, with a k that ends mid-stage (4104 = 64 * 64 + 8), tiles that
+    overhang m and n, split (with a workspace) and unsplit, and the relu epilogue. Against the
+    float64 product of the same bf16 values, rounded once."""
+    from limn_amd.dtypes import bf16_bits, bf16_values
+    from limn_amd.hip import runtime
+
+    a_vals = bf16_values(bf16_bits(rng.standard_normal((M, K)).astype(np.float32)))
+    b_vals = bf16_values(bf16_bits(rng.standard_normal((K, N)).astype(np.float32)))
+    a_store = a_vals if a_kcontig else np.ascontiguousarray(a_vals.T)
+    b_store = np.ascontiguousarray(b_vals.T) if b_kcontig else b_vals
+    a_m, a_k = (K, 1) if a_kcontig else (1, M)
+    b_k, b_n = (1, K) if b_kcontig else (N, 1)
+    lib = runtime.kernels()
+    a, b = hipdev.alloc(a_store.size * 2), hipdev.alloc(b_store.size * 2)
+    hipdev.copyin(a, bf16_bits(a_store))
+    hipdev.copyin(b, bf16_bits(b_store))
+    ws_bytes = lib.limn_hip_matmul_workspace(3, 1, M, N, K)
+    exact = a_vals.astype(np.float64) @ b_vals.astype(np.float64)
+    if relu:
+        exact = np.maximum(exact, 0.0)
+    for ws in ([None, hipdev.alloc(ws_bytes)] if ws_bytes else [None]):
+        c = hipdev.alloc(M * N * 2)
+        runtime.check_limn(lib.limn_hip_matmul(a.ptr, b.ptr, c.ptr, 3, 1, M, N, K, 0, a_m, a_k, 0, b_k, b_n, 0, N, 1,
+                                               1 if relu else 0, None if ws is None else ws.ptr,
+                                               0 if ws is None else ws_bytes, None))
+        hipdev.finish()
+        got = bf16_values(hipdev.copyout(c).view(np.uint16).reshape(M, N)).astype(np.float64)
+        np.testing.assert_allclose(got, exact, rtol=2**-7, atol=1e-2 * np.sqrt(K / 1024))
+
+
 @pytest.mark.parametrize("shape,dtype", [((8, 512, 96), float32), ((4, 300, 1536), bfloat16), ((2, 64, 200), float32)], ids=str)
 def test_column_reduce_over_batch_and_rows(hipdev, shape, dtype):
     """A bias gradient's shape: (b, t, c) summed over b and t. 64 cells per workgroup, rows
