@@ -358,13 +358,13 @@ def bench_c3(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
         "config": {"workload": "C3 bf16 4096^3 contraction + relu + bf16 store", "flop_per_step": flops},
         "kernels_ms": [round(float(t), 4) for t in per],
         "roofline": {
-            "kernel": "matmul_mfma (the contraction nest)",
+            "kernel": "matmul_dma (the contraction nest)",
             "bound": "mfma",
             "achieved": round(flops / (mm * 1e-3) / 1e12, 2),
             "peak": MFMA_BF16_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": round(flops / (mm * 1e-3) / MFMA_BF16_PEAK, 4),
-            "traffic": traffic("c3:matmul_mfma<BF16,256,256,true,false,0,false>"),
+            "traffic": traffic("c3:matmul_dma<BF16,256,256,true,false,0,false>"),
         },
         "cpu_baseline": None if cpu_s is None else {
             "value": round(2.0 * rows * n * n / cpu_s / 1e12, 6),

@@ -6,12 +6,26 @@
 // `A @ B` spelling of limn/tensor.py:486-496 lowers to exactly that nest (reference
 // limn/cuda_emit.py:376-505 detects the same shape and emits a SIMT tile).
 //
-// Tiling: a 256-thread workgroup computes a BM x BN tile (256 x 256, or 128 x 128 when the
-// larger tile would leave compute units idle); its 4 waves are 2 x 2, each owning
-// (BM/2) x (BN/2) = TM x TN accumulators of v_mfma_f32_32x32x16 (32x32 outputs, 16-deep k per
-// instruction), so per 16-deep step a wave reads TM + TN operands from LDS for TM * TN MFMAs.
-// K advances BK = 64 per stage through a double-buffered LDS: the next stage's global loads are
-// in registers while the current stage is multiplied.
+// Two kernels share the tiling. Output tiles are 256 x 256 (8 waves as 2 x 4, each owning
+// 128 x 64 = 4 x 2 accumulators of v_mfma_f32_32x32x16) or 128 x 128 (4 waves as 2 x 2, each
+// 64 x 64) when the larger tile would leave compute units idle. K advances BK = 64 per stage
+// through two LDS buffers.
+//
+// matmul_dma (k a multiple of 64): operands go from memory straight into LDS by
+// buffer_load ... lds (no VGPR staging, no LDS write instructions), the next stage's copy in
+// flight while the current one is multiplied. Tiles are unpadded and XOR-swizzled, 16-byte
+// chunk c of LDS row r at position c ^ f(r), so that the lane-linear DMA writes and the MFMA
+// operand reads are both conflict-free: a k-contiguous operand's tile is [rows][64] with
+// f(r) = (r >> 1) & 7 and each MFMA operand one ds_read_b128; an m- (or n-) contiguous operand's
+// tile is [64][rows] with f(k) = (k & 3) << 2 and each MFMA operand two transposing
+// ds_read_b64_tr_b16. Every wave's LDS reads for the next 16-deep k step are interleaved one per
+// MFMA of the current step. The two buffers of each operand are separate __shared__ arrays and
+// the loop is unrolled by two, so the compiler can see that a copy into the idle buffer never
+// aliases a read of the current one (it would otherwise wait for the copy before every read).
+//
+// matmul_mfma (any k that is a multiple of 8): operands are loaded into registers through a
+// buffer resource, the k tail past the end zeroed, and stored to padded LDS tiles ([rows][64 + 8]
+// and [64][rows + 32]) with the same operand reads.
 //
 // Split k: a contraction whose output has too few tiles to give every CU a workgroup and whose k
 // is long (a weight gradient sums over all batch rows) is cut into k slices; each workgroup
@@ -19,11 +33,8 @@
 // slices per element in slice order, applies the epilogue and rounds, so the result does not
 // depend on scheduling.
 //
-// LDS holds each operand in its memory orientation, copied with 16-byte loads through a buffer
-// resource (rows and k past the operand's end read as zeros, so the loop has no bounds tests). A
-// k-contiguous operand's tile is [rows][64 + 8] and each MFMA operand is one ds_read_b128 of a
-// row; an m- (or n-) contiguous operand's tile is [64][rows + 32] and each MFMA operand is two
-// transposing ds_read_b64_tr_b16. The paddings make every LDS read and write conflict-free.
+// Both kernels read operands through buffer resources: rows and k past an operand's end read as
+// zeros, so the loops carry no bounds tests; only the epilogue checks m and n.
 
 #include "matmul.h"
 
@@ -68,9 +79,8 @@ struct Operand {
     rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(extent * 2), 0x00020000);
   }
 
-  // the stage starting at k0; chunks at or past `depth` are zeroed when TAIL (a k-contiguous row
-  // runs on into the next row's elements there)
-  template <bool TAIL>
+  // the stage starting at k0; chunks at or past `depth` are zeroed (a k-contiguous row runs on
+  // into the next row's elements there)
   __device__ __forceinline__ void load(int k0, int depth) {
 #pragma unroll
     for (int s = 0; s < LOADS; s++) {
@@ -78,7 +88,7 @@ struct Operand {
       const int lrow = c / PER_ROW, lcol = (c % PER_ROW) * 8;
       const int off = KCONTIG ? (row0 + lrow) * stride + k0 + lcol : (k0 + lrow) * stride + row0 + lcol;
       r[s] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off * 2, 0, 0));
-      if (TAIL && KCONTIG && k0 + lcol >= depth) r[s] = zero8();
+      if (KCONTIG && k0 + lcol >= depth) r[s] = zero8();
     }
   }
 
@@ -106,7 +116,7 @@ struct Operand {
   }
 };
 
-template <typename T, int BM, int BN, bool A_K, bool B_K, int EPI, bool PARTIAL, bool TAIL>
+template <typename T, int BM, int BN, bool A_K, bool B_K, int EPI, bool PARTIAL>
 __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restrict__ a, const u16* __restrict__ b,
                                                              u16* __restrict__ c, float* __restrict__ ws, MatmulShape s,
                                                              int64_t chunk) {
@@ -139,12 +149,12 @@ __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restri
   OB sb(b + bz * s.b_batch, s.N, s.K, B_K ? s.b_n : s.b_k, n0);
   const int stages = (int)((k_hi - k_lo + BK - 1) / BK);
   const int kb = (int)k_lo, depth = (int)k_hi;
-  sa.template load<TAIL>(kb, depth);
-  sb.template load<TAIL>(kb, depth);
+  sa.load(kb, depth);
+  sb.load(kb, depth);
   sa.store(As[0]);
   sb.store(Bs[0]);
-  sa.template load<TAIL>(kb + BK, depth);
-  sb.template load<TAIL>(kb + BK, depth);
+  sa.load(kb + BK, depth);
+  sb.load(kb + BK, depth);
   __syncthreads();
   // one basic block per stage: the next stage's stores and the one after's loads are
   // unconditional (past the last stage they fill the idle buffer, or read zeros), so the compiler
@@ -167,8 +177,8 @@ __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restri
     }
     sa.store(As[cur ^ 1]);
     sb.store(Bs[cur ^ 1]);
-    sa.template load<TAIL>(kb + (st + 2) * BK, depth);
-    sb.template load<TAIL>(kb + (st + 2) * BK, depth);
+    sa.load(kb + (st + 2) * BK, depth);
+    sb.load(kb + (st + 2) * BK, depth);
     __syncthreads();
   }
 
@@ -209,6 +219,252 @@ __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restri
     }
 }
 
+// ---- matmul_dma ------------------------------------------------------------------------------
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// the s_waitcnt immediate that waits for every outstanding vector memory operation (vmcnt 0) and
+// leaves the other counters free
+constexpr int WAIT_VMEM = 0x0F70;
+
+// One operand's DMA copy into a swizzled LDS tile, and its MFMA operand reads.
+template <int ROWS, bool KCONTIG, int WAVES>
+struct DmaOperand {
+  static constexpr int RB = KCONTIG ? BK * 2 : ROWS * 2;  // bytes per LDS row
+  static constexpr int BYTES = (KCONTIG ? ROWS : BK) * RB;
+  static constexpr int PASSES = BYTES / (1024 * WAVES);   // 1 KB DMA instructions per wave per stage
+  static constexpr int RPI = 1024 / RB;                   // LDS rows one DMA instruction fills
+  static constexpr int READS = KCONTIG ? 1 : 2;           // LDS reads per MFMA operand
+  static_assert(PASSES * 1024 * WAVES == BYTES, "a stage is a whole number of DMA passes");
+  static __device__ __forceinline__ int swizzle(int r) { return KCONTIG ? (r >> 1) & 7 : (r & 3) << 2; }
+
+  const char* base;
+  int64_t extent, step, first;  // bytes from base the operand spans; bytes per stage; first stage
+  int voff[PASSES];
+
+  __device__ __forceinline__ DmaOperand(const u16* b, int64_t rows, int64_t depth, int64_t stride, int64_t row0,
+                                        int64_t k_lo, int wave, int lane) {
+    base = (const char*)b;
+    extent = 2 * (KCONTIG ? (rows - 1) * stride + depth : (depth - 1) * stride + rows);
+    step = KCONTIG ? 2 * BK : 2 * BK * stride;
+    first = k_lo / BK;
+#pragma unroll
+    for (int q = 0; q < PASSES; q++) {
+      // lane `lane` of this wave's q-th instruction fills position `pos` of LDS row r
+      const int r = (q * WAVES + wave) * RPI + lane / (RB / 16), pos = lane % (RB / 16);
+      const int c = pos ^ swizzle(r);
+      voff[q] = KCONTIG ? (int)(((row0 + r) * stride + c * 8) * 2) : (int)((r * stride + row0 + c * 8) * 2);
+    }
+  }
+
+  // this wave's share of stage st into `tile`; a stage past the end reads zeros (or the next
+  // slice's k) into the idle buffer, where nothing reads it
+  __device__ __forceinline__ void copy(char* tile, int st, int wave) const {
+    const int64_t off = (first + st) * step, left = extent - off;
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(base + off), (short)0, (int)(left > 0 ? left : 0), 0x00020000);
+#pragma unroll
+    for (int q = 0; q < PASSES; q++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(tile + (q * WAVES + wave) * 1024), 16, voff[q], 0, 0, 0);
+  }
+
+  // per-lane read offsets for the T 32-row blocks a wave multiplies, starting at row `row0`: by
+  // k step for a k-contiguous tile (the swizzle varies with k), by block otherwise
+  template <int T>
+  __device__ __forceinline__ void offsets(int row0, int lane, int* rd) const {
+    if (KCONTIG) {
+      const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+      for (int kk = 0; kk < BK / 16; kk++) rd[kk] = (row0 + r) * RB + (((2 * kk + h) ^ swizzle(r)) & 7) * 16;
+    } else {
+      const int g = lane >> 4, i = lane & 15, k = 8 * (g >> 1) + (i >> 2);
+#pragma unroll
+      for (int t = 0; t < T; t++) {
+        const int col = row0 + t * 32 + 16 * (g & 1) + 4 * (i & 3);
+        rd[t] = k * RB + ((col >> 3) ^ swizzle(k)) * 16 + (col & 7) * 2;
+      }
+    }
+  }
+
+  // the MFMA operand of block t at k step kk: lane l gets X[row0 + 32 t + l % 32][16 kk + 8 (l / 32) + j]
+  __device__ __forceinline__ u16x8 operand(const char* tile, const int* rd, int t, int kk) const {
+    if (KCONTIG) return *(const u16x8*)(tile + rd[kk] + t * 32 * RB);
+    // a transposing read gives lane i of each 16-lane group item j from the 8 bytes lane 4j + i/4
+    // addresses, element i % 4: lane r addresses k row 16 kk + 8 (l / 32) + r / 4 (+ 4 for the
+    // second read), columns row0 + 32 t + 16 ((l / 16) % 2) + 4 (r % 4)
+    const char* p = tile + rd[t] + kk * 16 * RB;
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)p);
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + 4 * RB));
+    return __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+};
+
+template <int BM>
+struct DmaTile {
+  static constexpr int WAVES = BM == 256 ? 8 : 4;
+  static constexpr int WN = WAVES / 2;  // waves along n; 2 along m
+};
+
+template <typename T, int BM, int BN, bool A_K, bool B_K, int EPI, bool PARTIAL>
+__global__ __launch_bounds__(64 * DmaTile<BM>::WAVES, 2) void matmul_dma(const u16* __restrict__ a, const u16* __restrict__ b,
+                                                                      u16* __restrict__ c, float* __restrict__ ws,
+                                                                      MatmulShape s, int64_t chunk, int wide) {
+  constexpr int WAVES = DmaTile<BM>::WAVES, WN = DmaTile<BM>::WN;
+  constexpr int WTM = BM / 2, WTN = BN / WN;  // one wave's output tile
+  constexpr int TM = WTM / 32, TN = WTN / 32, KS = BK / 16;
+  using DA = DmaOperand<BM, A_K, WAVES>;
+  using DB = DmaOperand<BN, B_K, WAVES>;
+  __shared__ __attribute__((aligned(1024))) char A0[DA::BYTES];
+  __shared__ __attribute__((aligned(1024))) char A1[DA::BYTES];
+  __shared__ __attribute__((aligned(1024))) char B0[DB::BYTES];
+  __shared__ __attribute__((aligned(1024))) char B1[DB::BYTES];
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n32 = lane & 31;
+  const int wm = wave / WN, wn = wave % WN;
+  const int64_t tiles_n = (s.N + BN - 1) / BN, tiles_m = (s.M + BM - 1) / BM;
+  const int64_t per_batch = tiles_m * tiles_n, per_slice = s.batch * per_batch;
+  // workgroup b runs on XCD b % 8: renumber so each XCD takes a contiguous run of tiles, and walk
+  // those in groups of 4 tile rows, so the rows and columns of operand an XCD's L2 holds are few
+  int64_t id = blockIdx.x;
+  if (gridDim.x % 8 == 0) id = (id % 8) * (gridDim.x / 8) + id / 8;
+  const int64_t slice = id / per_slice;
+  const int64_t bz = (id - slice * per_slice) / per_batch;
+  const int64_t t = id - slice * per_slice - bz * per_batch;
+  constexpr int64_t GROUP = 4;
+  const int64_t group = t / (GROUP * tiles_n), first = group * GROUP;
+  const int64_t rows = tiles_m - first < GROUP ? tiles_m - first : GROUP;
+  const int64_t tm = first + (t - group * GROUP * tiles_n) % rows, tn = (t - group * GROUP * tiles_n) / rows;
+  const int64_t m0 = tm * BM, n0 = tn * BN;
+  const int64_t k_lo = slice * chunk, k_hi = k_lo + chunk < s.K ? k_lo + chunk : s.K;
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+
+  const DA da(a + bz * s.a_batch, s.M, s.K, A_K ? s.a_m : s.a_k, m0, k_lo, wave, lane);
+  const DB db(b + bz * s.b_batch, s.N, s.K, B_K ? s.b_n : s.b_k, n0, k_lo, wave, lane);
+  int rda[A_K ? KS : TM], rdb[B_K ? KS : TN];
+  da.template offsets<TM>(wm * WTM, lane, rda);
+  db.template offsets<TN>(wn * WTN, lane, rdb);
+  const int stages = (int)((k_hi - k_lo) / BK);
+
+  u16x8 av[2][TM], bv[2][TN];
+  auto read = [&](const char* at, const char* bt, int kk, u16x8* ao, u16x8* bo) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TM; i++) ao[i] = da.operand(at, rda, i, kk);
+#pragma unroll
+    for (int j = 0; j < TN; j++) bo[j] = db.operand(bt, rdb, j, kk);
+  };
+  // one stage on (at, bt) while stage st + 1 is copied into (an, bn)
+  auto stage = [&](const char* at, const char* bt, char* an, char* bn, int st) __attribute__((always_inline)) {
+    da.copy(an, st + 1, wave);
+    db.copy(bn, st + 1, wave);
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) {
+      const int p = kk & 1;
+      if (kk + 1 < KS) read(at, bt, kk + 1, av[p ^ 1], bv[p ^ 1]);
+      // the B operand goes first: each accumulator then holds C transposed, 4 consecutive n per lane
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = T::mfma32(bv[p][j], av[p][i], acc[i][j]);
+    }
+    // the copy first, then each MFMA of a k step paired with one LDS read for the next
+    constexpr int RD = TM * DA::READS + TN * DB::READS, MF = TM * TN;
+    __builtin_amdgcn_sched_group_barrier(0x020, DA::PASSES + DB::PASSES, 0);
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) {
+      if (kk + 1 < KS) {
+#pragma unroll
+        for (int q = 0; q < (RD > MF ? RD : MF); q++) {
+          if (q < MF) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (q < RD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(WAIT_VMEM);  // this wave's part of stage st + 1 has landed
+    __syncthreads();                          // and every other wave's
+    read(an, bn, 0, av[0], bv[0]);
+  };
+
+  da.copy(A0, 0, wave);
+  db.copy(B0, 0, wave);
+  __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
+  __syncthreads();
+  read(A0, B0, 0, av[0], bv[0]);
+  for (int st = 0; st < stages; st += 2) {
+    stage(A0, B0, A1, B1, st);
+    if (st + 1 < stages) stage(A1, B1, A0, B0, st + 1);
+  }
+
+  // epilogue: lane holds C[m = wave row + 32 i + n32][n = wave column + 32 j + 8 q + 4 h + e],
+  // e = 0..3 in items 4 q + e
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+    const int64_t row = m0 + wm * WTM + i * 32 + n32;
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int64_t col = n0 + wn * WTN + j * 32 + 8 * q + 4 * h;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          v[e] = acc[i][j][4 * q + e];
+          if (!PARTIAL && EPI == MATMUL_EPILOGUE_RELU) v[e] = v[e] > 0.f ? v[e] : 0.f;
+        }
+        if (row >= s.M || col >= s.N) continue;
+        if (PARTIAL) {
+          float* w = ws + (slice * s.batch + bz) * s.M * s.N + row * s.N + col;
+          if (wide && col + 3 < s.N) {
+            *(f32x4*)w = f32x4{v[0], v[1], v[2], v[3]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+              if (col + e < s.N) w[e] = v[e];
+          }
+        } else {
+          u16* o = c + bz * s.c_batch + row * s.c_m + col * s.c_n;
+          if (wide && col + 3 < s.N) {
+            *(uint2*)o = make_uint2(T::pack2(v[0], v[1]), T::pack2(v[2], v[3]));
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+              if (col + e < s.N) o[e * s.c_n] = T::pack(v[e]);
+          }
+        }
+      }
+  }
+}
+
+// Every instance the launcher below can pick, instantiated explicitly: hipcc (ROCm 7.2) leaves
+// the host launch stubs of most implicitly instantiated instances of this kernel undefined,
+// which makes the library fail to load.
+#define LIMN_DMA_INSTANCE(T, BM, AK, BKC, EPI, P)                                                               \
+  template __global__ void matmul_dma<T, BM, BM, AK, BKC, EPI, P>(const u16* __restrict__, const u16* __restrict__, \
+                                                                  u16* __restrict__, float* __restrict__, MatmulShape, \
+                                                                  int64_t, int);
+#define LIMN_DMA_PARTIAL(T, BM, AK, BKC, EPI) LIMN_DMA_INSTANCE(T, BM, AK, BKC, EPI, false) LIMN_DMA_INSTANCE(T, BM, AK, BKC, EPI, true)
+#define LIMN_DMA_EPILOGUE(T, BM, AK, BKC) \
+  LIMN_DMA_PARTIAL(T, BM, AK, BKC, MATMUL_EPILOGUE_NONE) LIMN_DMA_PARTIAL(T, BM, AK, BKC, MATMUL_EPILOGUE_RELU)
+#define LIMN_DMA_LAYOUT(T, BM)                                                                   \
+  LIMN_DMA_EPILOGUE(T, BM, true, true) LIMN_DMA_EPILOGUE(T, BM, true, false) LIMN_DMA_EPILOGUE(T, BM, false, true) \
+  LIMN_DMA_EPILOGUE(T, BM, false, false)
+LIMN_DMA_LAYOUT(BF16, 256)
+LIMN_DMA_LAYOUT(BF16, 128)
+LIMN_DMA_LAYOUT(F16, 256)
+LIMN_DMA_LAYOUT(F16, 128)
+#undef LIMN_DMA_LAYOUT
+#undef LIMN_DMA_EPILOGUE
+#undef LIMN_DMA_PARTIAL
+#undef LIMN_DMA_INSTANCE
+
 // The slices of a split contraction, added per element in slice order, then the epilogue and the
 // store at c's strides.
 template <typename T, int EPI>
@@ -231,21 +487,26 @@ int launch_tile(const void* a, const void* b, void* c, const MatmulShape& s, con
   if (blocks > 0x7fffffff) return fail(LIMN_HIP_EUNSUPPORTED, "matmul: %lld workgroups exceed one launch", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(MM_THREADS);
   const bool tail = (s.K % BK) != 0 || (plan.chunk % BK) != 0;
-  if (plan.split == 1) {
-    if (tail)
-      hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, false, true>), grid, block, 0, stream, (const u16*)a,
-                         (const u16*)b, (u16*)c, (float*)nullptr, s, plan.chunk);
-    else
-      hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, false, false>), grid, block, 0, stream, (const u16*)a,
-                         (const u16*)b, (u16*)c, (float*)nullptr, s, plan.chunk);
+  if (!tail) {
+    // 8-byte stores of 4 consecutive n when the output rows are contiguous and 8-byte aligned
+    const bool wide = plan.split > 1 ? s.N % 4 == 0
+                                     : s.c_n == 1 && s.c_m % 4 == 0 && s.c_batch % 4 == 0 && (uintptr_t)c % 8 == 0;
+    const dim3 dma_block(64 * DmaTile<BM>::WAVES);
+    if (plan.split == 1) {
+      hipLaunchKernelGGL((matmul_dma<T, BM, BN, A_K, B_K, EPI, false>), grid, dma_block, 0, stream, (const u16*)a,
+                         (const u16*)b, (u16*)c, (float*)nullptr, s, plan.chunk, (int)wide);
+      return check_hip(hipGetLastError(), "launching the matmul kernel");
+    }
+    hipLaunchKernelGGL((matmul_dma<T, BM, BN, A_K, B_K, EPI, true>), grid, dma_block, 0, stream, (const u16*)a,
+                       (const u16*)b, (u16*)c, (float*)ws, s, plan.chunk, (int)wide);
+  } else if (plan.split == 1) {
+    hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, false>), grid, block, 0, stream, (const u16*)a,
+                       (const u16*)b, (u16*)c, (float*)nullptr, s, plan.chunk);
     return check_hip(hipGetLastError(), "launching the matmul kernel");
+  } else {
+    hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, true>), grid, block, 0, stream, (const u16*)a,
+                       (const u16*)b, (u16*)c, (float*)ws, s, plan.chunk);
   }
-  if (tail)
-    hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, true, true>), grid, block, 0, stream, (const u16*)a,
-                       (const u16*)b, (u16*)c, (float*)ws, s, plan.chunk);
-  else
-    hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, true, false>), grid, block, 0, stream, (const u16*)a,
-                       (const u16*)b, (u16*)c, (float*)ws, s, plan.chunk);
   const int rc = check_hip(hipGetLastError(), "launching the split matmul kernel");
   if (rc != LIMN_HIP_OK) return rc;
   const int64_t total = s.batch * s.M * s.N;

@@ -399,11 +399,24 @@ def test_split_k_without_workspace_runs_unsplit(hipdev):
 
 @pytest.mark.parametrize("a_kcontig", [True, False], ids=["a-k", "a-m"])
 @pytest.mark.parametrize("b_kcontig", [True, False], ids=["b-k", "b-n"])
-@pytest.mark.parametrize("M,N,K,relu", [(256, 128, 4104, False), (200, 72, 1000, True), (520, 264, 72, False)], ids=str)
+@pytest.mark.parametrize(
+    "M,N,K,relu",
+    [
+        (256, 128, 4104, False),
+        (200, 72, 1000, True),
+        (520, 264, 72, False),
+        (256, 128, 4096, False),
+        (200, 72, 1024, True),
+        (520, 264, 128, False),
+        (4096, 4096, 64, True),
+    ],
+    ids=str,
+)
 def test_matmul_layouts_through_the_c_abi(hipdev, a_kcontig, b_kcontig, M, N, K, relu):
-    """Every operand orientation, with a k that ends mid-stage (4104 = 64 * 64 + 8), tiles that
-    overhang m and n, split (with a workspace) and unsplit, and the relu epilogue. Against the
-    float64 product of the same bf16 values, rounded once."""
+    """Every operand orientation through both kernels: k that ends mid-stage (4104 = 64 * 64 + 8,
+    1000, 72) takes the register-staged kernel, k a multiple of 64 the DMA kernel; tiles that
+    overhang m and n, 128- and 256-tiles, split (with a workspace) and unsplit, and the relu
+    epilogue. Against the float64 product of the same bf16 values, rounded once."""
     from limn_amd.dtypes import bf16_bits, bf16_values
     from limn_amd.hip import runtime
 
