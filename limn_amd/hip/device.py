@@ -26,7 +26,8 @@ from limn_amd.dtypes import ABI_CODE
 from limn_amd.hip import runtime
 from limn_amd.hip.runtime import DEVICE_TO_DEVICE, DEVICE_TO_HOST, HOST_TO_DEVICE, check, check_limn
 from limn_amd.jit import Buffer, CompiledDevice, Runner
-from limn_amd.ops import FLOATS, Node, accumulate_in
+from limn_amd.ops import FLOATS, Node, Op, accumulate_in
+from limn_amd.schedule import realized
 
 SDPA, SDPA_BWD_Q, SDPA_BWD_KV = "sdpa", "sdpa_bwd_q", "sdpa_bwd_kv"
 
@@ -52,6 +53,7 @@ class HipDevice(CompiledDevice):
     """Construct through set_device("hip"), which checks the runtime and the GPU first."""
 
     def __init__(self) -> None:
+        self.plan_kept: set | None = None  # set by plan_of for runners(), see there
         super().__init__()
         api = runtime.hip()
         assert api is not None, "construct via set_device('hip'), which explains what is missing"
@@ -131,6 +133,16 @@ class HipDevice(CompiledDevice):
 
     def finish(self) -> None:
         check(self.api.hipDeviceSynchronize(), "waiting for the batch")
+
+    def plan_of(self, order: list[Node], position: dict[Node, int], sinks: list[Node]):
+        """The executor's plan_of, with the buffers that must hold their values recorded for
+        runners(): the sinks and every CUSTOM src. runners() sees only the non-CUSTOM nests, and
+        a contraction's epilogue may absorb a relu nest only when no one else reads the sum."""
+        self.plan_kept = {realized(s) for s in sinks} | {realized(src) for n in order if n.op is Op.CUSTOM for src in n.srcs}
+        try:
+            return super().plan_of(order, position, sinks)
+        finally:
+            self.plan_kept = None
 
     def runners(self, nests: list[LoopNest]) -> list[Runner]:
         from limn_amd.hip.emit import nest_runners

@@ -714,13 +714,77 @@ def _launcher(dev, fn: int, launch: Launch, nin: int):
     return run
 
 
+def is_relu(nest: LoopNest) -> bool:
+    """Whether an elementwise nest is exactly limn's relu of its one input, read at the cell it
+    stores: out = where(0 < x, x, 0) (reference limn/tensor.py:365-366), nothing else."""
+    body = [i for i in nest.instrs if i.opcode not in (Opcode.LOOP, Opcode.ENDLOOP)]
+    if len(nest.kernel.inputs) != 1 or any(i.opcode is Opcode.ACCUM for i in body):
+        return False
+    loads = [i for i in body if i.opcode is Opcode.LOAD]
+    stores = [i for i in body if i.opcode is Opcode.STORE]
+    if len(loads) != 1 or len(stores) != 1 or loads[0].arg[0] != "in0" or loads[0].arg[2].bounds:
+        return False
+    x, index = loads[0].dest, stores[0].arg[1]
+    if loads[0].arg[1] != index:
+        return False
+    zeros = {i.dest for i in body if i.opcode is Opcode.CONST and i.arg[0] == 0 and not i.arg[1].bounds}
+    arith = [i for i in body if i.opcode is Opcode.ARITH]
+    if len(body) != len(loads) + len(stores) + len(arith) + len(zeros) or len(arith) != 2:
+        return False
+    cmp, sel = arith
+    return (
+        cmp.arg is Op.CMPLT and cmp.srcs[0] in zeros and cmp.srcs[1] == x
+        and sel.arg is Op.WHERE and sel.srcs[0] == cmp.dest and sel.srcs[1] == x and sel.srcs[2] in zeros
+        and stores[0].srcs == (sel.dest,)
+    )
+
+
+def epilogue_pairs(nests: list[LoopNest], plans: list[Planned], kept: set | None) -> dict[int, int]:
+    """Relu nests to run as their contraction's epilogue: {contraction nest: relu nest}.
+
+    The relu crosses a scheduler cut (the SUM is its own kernel), so it may only move into the
+    contraction's store when nothing else needs the SUM's buffer: the relu nest is its only
+    reader among the plan's nests, and it is neither a sink nor read by a CUSTOM call (`kept`,
+    recorded by the device's plan_of; None when unknown, which fuses nothing)."""
+    if kept is None:
+        return {}
+    pairs: dict[int, int] = {}
+    for i, plan in enumerate(plans):
+        if plan.contraction is None:
+            continue
+        total = nests[i].kernel.target
+        if total in kept:
+            continue
+        readers = [j for j, n in enumerate(nests) if any(src is total for src in n.kernel.inputs)]
+        if len(readers) != 1 or readers[0] <= i:
+            continue
+        j = readers[0]
+        relu = nests[j].kernel.target
+        if is_relu(nests[j]) and relu.dtype == total.dtype and math.prod(relu.shape) == math.prod(total.shape):
+            pairs[i] = j
+    return pairs
+
+
 def nest_runners(dev, nests: list[LoopNest]):
-    """Compile every nest of a plan into one hipRTC program; one runner per nest, in order."""
+    """Compile every nest of a plan into one hipRTC program; one runner per nest, in order. A
+    contraction whose only reader is a relu nest runs as one MFMA launch with a relu epilogue,
+    from the relu nest's runner (see epilogue_pairs)."""
     plans = [plan_nest(n) for n in nests]
+    pairs = epilogue_pairs(nests, plans, getattr(dev, "plan_kept", None))
+    fused = {j: i for i, j in pairs.items()}
+    for j in fused:
+        plans[j] = Planned("", [], notes={"epilogue of": nests[fused[j]].name})
     names = [launch.name for p in plans for launch in p.launches]
     functions = runtime.load_functions(PRELUDE + "\n".join(p.source for p in plans), names) if names else {}
     runners = []
-    for nest, plan in zip(nests, plans):
+    operands: dict[int, list] = {}  # a fused contraction's inputs, from its call to its relu's
+    for k, (nest, plan) in enumerate(zip(nests, plans)):
+        if k in pairs:
+            runners.append(_stash_runner(operands, k))
+            continue
+        if k in fused:
+            runners.append(_epilogue_runner(dev, plans[fused[k]].contraction, operands, fused[k]))
+            continue
         if plan.contraction is not None:
             runners.append(_contraction_runner(dev, plan.contraction))
             continue
@@ -733,23 +797,54 @@ def nest_runners(dev, nests: list[LoopNest]):
     return runners
 
 
-def _contraction_runner(dev, con: Contraction):
+def _matmul_launcher(dev, con: Contraction, epilogue: int):
+    """launch(inputs, out_ptr): the contraction through limn_hip_matmul."""
     from limn_amd.dtypes import ABI_CODE
 
     lib = dev.lib
     code = ABI_CODE[con.dtype]
     size = con.dtype.itemsize
-    shape = (code, con.batch, con.M, con.N, con.K, con.a_batch, con.a_m, con.a_k, con.b_batch, con.b_k, con.b_n, con.c_batch, con.c_m, con.c_n, 0)
+    shape = (code, con.batch, con.M, con.N, con.K, con.a_batch, con.a_m, con.a_k, con.b_batch, con.b_k, con.b_n, con.c_batch, con.c_m, con.c_n, epilogue)
     ws_bytes = int(lib.limn_hip_matmul_workspace(code, con.batch, con.M, con.N, con.K))
     held: list = []  # the split-k workspace, allocated on first use and kept with the runner
 
-    def run(inputs: list, outs: list) -> None:
+    def launch(inputs: list, out: int) -> None:
         if ws_bytes and not held:
             held.append(dev._alloc(ws_bytes))
         a = inputs[con.a_input].ptr + con.a_offset * size
         b = inputs[con.b_input].ptr + con.b_offset * size
         ws = held[0].ptr if held else None
-        runtime.check_limn(lib.limn_hip_matmul(a, b, outs[0].ptr, *shape, ws, ws_bytes, None))
+        runtime.check_limn(lib.limn_hip_matmul(a, b, out, *shape, ws, ws_bytes, None))
+
+    return launch
+
+
+def _contraction_runner(dev, con: Contraction):
+    launch = _matmul_launcher(dev, con, 0)
+
+    def run(inputs: list, outs: list) -> None:
+        launch(inputs, outs[0].ptr)
+
+    return run
+
+
+def _stash_runner(operands: dict, k: int):
+    """A fused contraction's own call: keep its operands for the relu nest's call, launch nothing
+    (its output buffer is never read)."""
+
+    def run(inputs: list, outs: list) -> None:
+        operands[k] = inputs
+
+    return run
+
+
+def _epilogue_runner(dev, con: Contraction, operands: dict, k: int):
+    """The relu nest's call: the contraction of nest k with a relu epilogue, stored into this
+    nest's output. Its layout is the contraction's: the relu reads and writes cell for cell."""
+    launch = _matmul_launcher(dev, con, 1)
+
+    def run(inputs: list, outs: list) -> None:
+        launch(operands.pop(k), outs[0].ptr)
 
     return run
 

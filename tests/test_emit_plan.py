@@ -1,0 +1,101 @@
+"""The hip device's plan-time decisions that need no GPU: which nests are dense contractions, and
+when a relu nest may run as its contraction's epilogue (reference limn/tensor.py:365-366 spells
+relu; the scheduler cuts after the SUM, limn/schedule.py:46-141, so the fusion is the device's to
+make and only when nothing else reads the sum). The library is loaded for its layout check only;
+no kernel runs."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from limn_amd import device as limn_device
+from limn_amd.codegen import lower_all
+from limn_amd.ops import Op, bfloat16, float32, topological
+from limn_amd.schedule import realized, schedule
+from limn_amd.tensor import Tensor
+
+emit = pytest.importorskip("limn_amd.hip.emit")
+
+rng = np.random.default_rng(5)
+
+
+@pytest.fixture(autouse=True)
+def on_numpy():
+    limn_device.set_device("numpy")
+    yield
+
+
+def lowered(sinks: list[Tensor]):
+    nodes = [t.node for t in sinks]
+    order = topological(nodes)
+    nests = lower_all(nodes, order, schedule(nodes, order))
+    kept = {realized(s) for s in nodes} | {realized(src) for n in order if n.op is Op.CUSTOM for src in n.srcs}
+    return nests, kept
+
+
+def operands(m: int = 64, k: int = 64, n: int = 48):
+    a = Tensor(rng.standard_normal((m, k)).astype(np.float32), dtype=bfloat16)
+    b = Tensor(rng.standard_normal((k, n)).astype(np.float32), dtype=bfloat16)
+    return a, b
+
+
+def pairs_of(sinks: list[Tensor]) -> dict[int, int]:
+    nests, kept = lowered(sinks)
+    return emit.epilogue_pairs(nests, [emit.plan_nest(n) for n in nests], kept)
+
+
+def test_relu_nest_is_recognised():
+    a, b = operands()
+    nests, _ = lowered([(a @ b).relu()])
+    assert [emit.is_relu(n) for n in nests] == [False, True]
+
+
+@pytest.mark.parametrize(
+    "spell",
+    [lambda x: x * 2.0, lambda x: (x < 0).where(x, x * 0.0), lambda x: (x > 1).where(x, x * 0.0), lambda x: x.exp()],
+    ids=["scale", "negative part", "threshold 1", "exp"],
+)
+def test_other_elementwise_nests_are_not_relu(spell):
+    a, b = operands()
+    nests, _ = lowered([spell(a @ b)])
+    assert not emit.is_relu(nests[-1])
+
+
+def test_relu_of_a_contraction_becomes_its_epilogue():
+    a, b = operands()
+    assert pairs_of([(a @ b).relu()]) == {0: 1}
+
+
+def test_no_fusion_when_the_sum_is_also_a_sink():
+    a, b = operands()
+    mm = a @ b
+    assert pairs_of([mm, mm.relu()]) == {}
+
+
+def test_no_fusion_when_another_nest_reads_the_sum():
+    a, b = operands()
+    mm = a @ b
+    assert pairs_of([mm.relu() + mm.exp()]) == {}
+
+
+def test_no_fusion_when_a_custom_call_reads_the_sum():
+    a, b = operands(64, 64, 64)
+    mm = (a @ b).reshape(1, 64, 64)
+    out = mm.relu().reshape(1, 64, 64).attention(mm, mm)
+    nests, kept = lowered([out])
+    plans = [emit.plan_nest(n) for n in nests]
+    assert any(p.contraction is not None for p in plans)
+    assert emit.epilogue_pairs(nests, plans, kept) == {}
+
+
+def test_no_fusion_without_a_record_of_readers():
+    a, b = operands()
+    nests, _ = lowered([(a @ b).relu()])
+    assert emit.epilogue_pairs(nests, [emit.plan_nest(n) for n in nests], None) == {}
+
+
+def test_float32_sum_is_not_a_contraction():
+    a = Tensor(rng.standard_normal((64, 64)).astype(np.float32), dtype=float32)
+    nests, _ = lowered([(a @ a).relu()])
+    assert all(emit.plan_nest(n).contraction is None for n in nests)

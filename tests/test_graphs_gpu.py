@@ -345,6 +345,28 @@ def test_config3_full_size(hipdev):
     np.testing.assert_allclose(got, want, rtol=2e-2, atol=2e-2)
 
 
+@pytest.mark.parametrize("m,n,k", [(200, 72, 1024), (256, 128, 4096), (96, 40, 200)], ids=["dma", "split-k", "k-tail"])
+def test_relu_epilogue_matches_the_separate_relu_bit_for_bit(hipdev, m, n, k):
+    """(A @ B).relu() as one MFMA launch with a relu epilogue (the relu nest is the sum's only
+    reader) against the same graph with the sum also a sink, which keeps the relu nest separate:
+    rounding commutes with relu, so the bits agree. And both against the float64 closed form."""
+    from limn_amd.dtypes import bf16_bits, bf16_values
+
+    a_vals = bf16_values(bf16_bits(rng.standard_normal((m, k)).astype(np.float32)))
+    b_vals = bf16_values(bf16_bits(rng.standard_normal((k, n)).astype(np.float32)))
+    a, b = Tensor(a_vals, dtype=bfloat16), Tensor(b_vals, dtype=bfloat16)
+    mm = a @ b
+    relu = mm.relu()
+    fused = hipdev.copyout(hipdev.execute([relu.node])[0]).view(np.uint16)
+    total, separate = hipdev.execute([mm.node, relu.node])
+    separate = hipdev.copyout(separate).view(np.uint16)
+    np.testing.assert_array_equal(fused, separate)
+    got = bf16_values(fused.reshape(m, n)).astype(np.float64)
+    exact = np.maximum(a_vals.astype(np.float64) @ b_vals.astype(np.float64), 0.0)
+    np.testing.assert_allclose(got, exact, rtol=2**-7, atol=1e-2 * np.sqrt(k / 1024))
+    assert (got >= 0).all()
+
+
 def test_weight_gradient_is_one_split_k_contraction(hipdev):
     """A weight gradient sums over batch and rows together (K = 8 * 512 = 4096) into a 256 x 128
     output: one contraction, split in k (the output is two 128-tiles), its slices added in order.
@@ -449,9 +471,11 @@ def test_column_reduce_over_batch_and_rows(hipdev, shape, dtype):
     """A bias gradient's shape: (b, t, c) summed over b and t. 64 cells per workgroup, rows
     split into parts; a partial last tile (c % 64) and a single-part case (few rows) included."""
     x = Tensor(rng.standard_normal(shape).astype(np.float32), dtype=dtype)
-    tol = 1e-4 if dtype is float32 else 2e-2
-    check(hipdev, x.sum(axis=(0, 1)), rtol=tol, atol=tol)
-    check(hipdev, (x * x).sum(axis=(0, 1), keepdim=True), rtol=tol, atol=tol)
+    tol = 1e-5 if dtype is float32 else 2e-2
+    # a column of N(0, 1) can total ~1 while its partial sums reach ~sqrt(rows): the error is
+    # bounded relative to the largest total, not to each
+    check(hipdev, x.sum(axis=(0, 1)), worst=tol)
+    check(hipdev, (x * x).sum(axis=(0, 1), keepdim=True), worst=tol)
 
 
 def test_column_max_keeps_nan(hipdev):
