@@ -31,6 +31,8 @@
 // 32x32 accumulator layout (CDNA3/CDNA4 matrix cores): lane l, item i holds
 // row 8*(i/4) + 4*(l/32) + i%4, column l%32.
 
+#include <type_traits>
+
 #include "sdpa.h"
 
 namespace limn {
@@ -47,6 +49,22 @@ __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+// The (head, row block) a workgroup owns. Workgroup id runs on XCD id % 8: each XCD is given a
+// contiguous run of ids, heads major, so a head's blocks run together on one XCD and share its
+// L2's copy of the streamed operands (4 MB of L2 per XCD; a head's K and V, or Q and dO, are 2 MB
+// at t = 4096, D = 128). Blocks of a head come in order; the kernels number them so that the
+// longest (under causal) go first.
+__device__ __forceinline__ void head_and_block(int64_t batch, int64_t nblocks, int64_t& b, int64_t& blk) {
+  if (gridDim.x % 8 == 0) {
+    const int64_t id = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
+    b = id / nblocks;
+    blk = id % nblocks;
+  } else {
+    b = blockIdx.x % batch;
+    blk = blockIdx.x / batch;
+  }
+}
 
 // ---- LDS tiles -------------------------------------------------------------------------------
 // A streamed tile is TILE rows x D elements, rows padded to D + 8 elements (a 16-byte chunk more
@@ -233,8 +251,9 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
   // uniform branches instead of exec-masked ones
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
   const int64_t nqb = (t_q + ROWS - 1) / ROWS;
-  const int64_t b = blockIdx.x % batch;
-  const int64_t qb = nqb - 1 - blockIdx.x / batch;  // causal: the longest rows go first
+  int64_t b, blk;
+  head_and_block(batch, nqb, b, blk);
+  const int64_t qb = nqb - 1 - blk;  // causal: the longest rows go first
   const int q0 = (int)qb * ROWS, wq0 = q0 + wave * 32 * NT;
   const Rows qrows(q + b * (int64_t)t_q * D, t_q, D);
   const Rows krows(k + b * (int64_t)t_k * D, t_k, D), vrows(v + b * (int64_t)t_k * D, t_k, D);
@@ -373,8 +392,9 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_bwd_q_mfma(cons
   // uniform branches instead of exec-masked ones
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
   const int64_t nqb = (t_q + ROWS - 1) / ROWS;
-  const int64_t b = blockIdx.x % batch;
-  const int64_t qb = nqb - 1 - blockIdx.x / batch;
+  int64_t b, blk;
+  head_and_block(batch, nqb, b, blk);
+  const int64_t qb = nqb - 1 - blk;  // causal: the longest rows go first
   const int q0 = (int)qb * ROWS, wq0 = q0 + wave * 32 * NT;
   const Rows qrows(q + b * (int64_t)t_q * D, t_q, D), orows(dout + b * (int64_t)t_q * D, t_q, D);
   const Rows krows(k + b * (int64_t)t_k * D, t_k, D), vrows(v + b * (int64_t)t_k * D, t_k, D);
@@ -496,8 +516,8 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_mfma(const u16* __rest
   // the wave index in a scalar register: the per-wave tile bounds and causal tests below are then
   // uniform branches instead of exec-masked ones
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
-  const int64_t b = blockIdx.x % batch;
-  const int64_t kb = blockIdx.x / batch;  // causal: the first keys are seen by the most queries
+  int64_t b, kb;  // causal: the first keys are seen by the most queries
+  head_and_block(batch, (t_k + ROWS - 1) / ROWS, b, kb);
   const int k0 = (int)kb * ROWS, wk0 = k0 + wave * 32 * NT;
   const Rows qrows(q + b * (int64_t)t_q * D, t_q, D), orows(dout + b * (int64_t)t_q * D, t_q, D);
   const Rows krows(k + b * (int64_t)t_k * D, t_k, D), vrows(v + b * (int64_t)t_k * D, t_k, D);
@@ -655,6 +675,242 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_mfma(const u16* __rest
   }
 }
 
+// ---- dK/dV pass at D = 128: streamed tiles copied straight into LDS ----------------------------
+// The streamed Q and dO tiles go from memory to LDS by buffer_load ... lds (no staging registers,
+// no LDS write instructions), into unpadded tiles whose 16-byte chunk c of row r sits at position
+// c ^ swz(r): lane-linear 1 KB DMA writes, and conflict-free row-operand and transposing reads
+// (measured LDS model above). Each buffer is its own __shared__ array and tiles alternate between
+// them in an unrolled pair, so the compiler sees that a copy into the idle buffer never aliases
+// a read of the current one. The tiles that need masking (a causal wave's first two, holding
+// every query before its last key, a last tile past t_q, every tile under a key mask) run a
+// separate instance of the tile body from the unmasked ones, so each loop is one basic block
+// whose LDS reads the scheduler can interleave with the MFMAs.
+
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr int WAIT_VMEM = 0x0F70;  // s_waitcnt immediate: vmcnt(0), other counters free
+
+__device__ __forceinline__ int swz128(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// rows [row0, row0 + TILE) of a (rows x 128) matrix into a swizzled tile, this wave's quarter
+struct DmaTile128 {
+  static constexpr int RB = 256, PASSES = TILE * RB / 1024 / WAVES;
+  const char* base;
+  int64_t bytes;
+  int voff[PASSES];
+  __device__ __forceinline__ DmaTile128(const u16* m, int rows, int wave, int lane) {
+    base = (const char*)m;
+    bytes = (int64_t)rows * RB;
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+      const int r = (p * WAVES + wave) * (1024 / RB) + lane / (RB / 16), pos = lane % (RB / 16);
+      voff[p] = r * RB + ((pos ^ swz128(r)) * 16);
+    }
+  }
+  // rows past the end read as zeros (the resource ends at the matrix)
+  __device__ __forceinline__ void copy(u16* tile, int row0, int wave) const {
+    const int64_t off = (int64_t)row0 * RB, left = bytes - off;
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(base + off), (short)0, (int)(left > 0 ? left : 0), 0x00020000);
+#pragma unroll
+    for (int p = 0; p < PASSES; p++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)((char*)tile + (p * WAVES + wave) * 1024), 16, voff[p], 0, 0, 0);
+  }
+};
+
+// per-lane byte offsets into a swizzled tile: row operands (row n of a 32-row step, chunk 2 ds + h)
+// by ds; transposing reads (rows 4 h + 8 jj + i / 4, columns 32 dt + 16 (g % 2) + 4 (i % 4)) by
+// (dt, jj). Every read is then one of these plus a compile-time offset.
+struct SwzReads128 {
+  int row[8], tr[4][2];
+  __device__ __forceinline__ SwzReads128(int lane) {
+    const int n = lane & 31, h = lane >> 5, g = lane >> 4, i = lane & 15;
+#pragma unroll
+    for (int ds = 0; ds < 8; ds++) row[ds] = n * 256 + (((2 * ds + h) ^ swz128(n)) * 16);
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) {
+        const int r = 4 * h + 8 * jj + (i >> 2), col = dt * 32 + 16 * (g & 1) + 4 * (i & 3);
+        tr[dt][jj] = r * 256 + (((col >> 3) ^ swz128(r)) * 16) + (col & 7) * 2;
+      }
+  }
+  // row operand: elements 16 ds + 8 h .. + 7 of row sub * 32 + n
+  __device__ __forceinline__ u16x8 rows(const u16* tile, int sub, int ds) const {
+    return *(const u16x8*)((const char*)tile + row[ds] + sub * 32 * 256);
+  }
+  // transposed operand of rows k0 .. k0 + 15, columns 32 dt .. + 31 (see read_transposed)
+  __device__ __forceinline__ u16x8 transposed(const u16* tile, int k0, int dt) const {
+    const char* p = (const char*)tile + k0 * 256;
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + tr[dt][0]));
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + tr[dt][1]));
+    return __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+};
+
+// one 64-query tile against the wave's 32 resident keys: per 32-query step, S = Q K^T and
+// dP = dO V^T, the probabilities and dS, then dV^T += dO^T P and dK^T += Q^T dS
+template <typename T, bool CAUSAL, bool MASK, bool EDGE>
+__device__ __forceinline__ void kv_tile128(const u16* Qb, const u16* Ob, const float* Lb, const float* Db,
+                                           const SwzReads128& ad, int r0, int wk0, int t_q, float c2, float scale,
+                                           bool live, const u16x8 (&kf)[8], const u16x8 (&vf)[8], f32x16 (&gk)[4],
+                                           f32x16 (&gv)[4]) {
+  const int lane = threadIdx.x & 63, h = lane >> 5, n = lane & 31;
+#pragma unroll
+  for (int sub = 0; sub < 2; sub++) {
+    const int s0 = r0 + sub * 32;
+    f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+    for (int ds = 0; ds < 8; ds++) {
+      s = T::mfma32(ad.rows(Qb, sub, ds), kf[ds], s);
+      dp = T::mfma32(ad.rows(Ob, sub, ds), vf[ds], dp);
+    }
+    f32x4 l4[4], d4[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      l4[g] = *(const f32x4*)(Lb + sub * 32 + 8 * g + 4 * h);
+      d4[g] = *(const f32x4*)(Db + sub * 32 + 8 * g + 4 * h);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) s[i] = fast_exp2(fmaf(s[i], c2, -l4[i >> 2][i & 3]));
+    if (EDGE) {
+      const int key = wk0 + n;
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const int qq = s0 + 8 * (i >> 2) + 4 * h + (i & 3);
+        bool hide = (qq >= t_q) | !live;
+        if (CAUSAL) hide |= qq < key;
+        s[i] = hide ? 0.f : s[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) dp[i] = s[i] * fmaf(dp[i], scale, -d4[i >> 2][i & 3]);
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const u16x8 pb = pack8<T>(s, 8 * c), gb = pack8<T>(dp, 8 * c);
+#pragma unroll
+      for (int dt = 0; dt < 4; dt++) {
+        gv[dt] = T::mfma32(ad.transposed(Ob, sub * 32 + 16 * c, dt), pb, gv[dt]);
+        gk[dt] = T::mfma32(ad.transposed(Qb, sub * 32 + 16 * c, dt), gb, gk[dt]);
+      }
+    }
+  }
+  // per step: the S/dP MFMAs with their 16 row reads and the 8 statistics reads (4 ahead), the
+  // softmax, then the dV/dK MFMAs with their 32 transposing reads (4 ahead)
+#pragma unroll
+  for (int sub = 0; sub < 2; sub++) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int q = 0; q < 10; q++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 200, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int q = 0; q < 14; q++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  }
+}
+
+template <typename T, bool CAUSAL, bool MASK>
+__global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_dma(const u16* __restrict__ q, const u16* __restrict__ k,
+                                                              const u16* __restrict__ v, const u16* __restrict__ dout,
+                                                              const float* __restrict__ lse,
+                                                              const float* __restrict__ delta,
+                                                              const u16* __restrict__ mask, u16* __restrict__ dk,
+                                                              u16* __restrict__ dv, int64_t batch, int t_q, int t_k,
+                                                              float scale) {
+  constexpr int D = 128, ROWS = 128;
+  __shared__ __attribute__((aligned(1024))) u16 Q0[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 Q1[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 O0[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 O1[TILE * D];
+  __shared__ __attribute__((aligned(16))) float L0[TILE], L1[TILE], D0[TILE], D1[TILE];
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
+  int64_t b, kb;  // causal: the first keys are seen by the most queries
+  head_and_block(batch, (t_k + ROWS - 1) / ROWS, b, kb);
+  const int k0 = (int)kb * ROWS, wk0 = k0 + wave * 32;
+  const Rows krows(k + b * (int64_t)t_k * D, t_k, D), vrows(v + b * (int64_t)t_k * D, t_k, D);
+  const DmaTile128 qd(q + b * (int64_t)t_q * D, t_q, wave, lane), od(dout + b * (int64_t)t_q * D, t_q, wave, lane);
+  const SwzReads128 ad(lane);
+  const float c2 = scale * LOG2E;
+
+  u16x8 kf[8], vf[8];
+  f32x16 gk[4], gv[4];
+  const int key = wk0 + n;
+#pragma unroll
+  for (int ds = 0; ds < 8; ds++) {
+    kf[ds] = krows.load8(key * D + ds * 16 + 8 * h);
+    vf[ds] = vrows.load8(key * D + ds * 16 + 8 * h);
+  }
+  bool live = key < t_k;
+  if (MASK) live = live & (T::unpack(mask[b * (int64_t)t_k + (key < t_k ? key : t_k - 1)]) != 0.f);
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++) {
+    gk[dt] = zero16();
+    gv[dt] = zero16();
+  }
+  const int qstart = CAUSAL ? k0 : 0;  // a causal key is seen by queries at or after it
+  const int ntiles = qstart < t_q ? (t_q - qstart + TILE - 1) / TILE : 0;
+
+  // a tile's statistics (lse * log2 e and delta * scale of its queries), by the first wave
+  auto stats = [&](int r0, float* L, float* Dl) __attribute__((always_inline)) {
+    if (threadIdx.x < TILE) {
+      const int qq = r0 + (int)threadIdx.x;
+      L[threadIdx.x] = qq < t_q ? lse[b * (int64_t)t_q + qq] * LOG2E : 0.f;
+      Dl[threadIdx.x] = qq < t_q ? delta[b * (int64_t)t_q + qq] * scale : 0.f;
+    }
+  };
+  // tile it from (Qc, Oc, Lc, Dc) while tile it + 1 is copied into the idle buffers (every wave
+  // left them at the last barrier), then the wait for the copy and the barrier
+  auto step = [&](auto edge, int it, const u16* Qc, const u16* Oc, const float* Lc, const float* Dc, u16* Qn, u16* On,
+                  float* Ln, float* Dn) __attribute__((always_inline)) {
+    const int r0 = qstart + it * TILE;
+    qd.copy(Qn, r0 + TILE, wave);
+    od.copy(On, r0 + TILE, wave);
+    stats(r0 + TILE, Ln, Dn);
+    kv_tile128<T, CAUSAL, MASK, decltype(edge)::value>(Qc, Oc, Lc, Dc, ad, r0, wk0, t_q, c2, scale, live, kf, vf, gk, gv);
+    __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
+    __syncthreads();
+  };
+  // tiles [from, to) with one body, from even: tile it is in buffer it % 2
+  auto run = [&](auto edge, int from, int to) __attribute__((always_inline)) {
+    int it = from;
+    for (; it + 1 < to; it += 2) {
+      step(edge, it, Q0, O0, L0, D0, Q1, O1, L1, D1);
+      step(edge, it + 1, Q1, O1, L1, D1, Q0, O0, L0, D0);
+    }
+    if (it < to) step(edge, it, Q0, O0, L0, D0, Q1, O1, L1, D1);
+  };
+  if (ntiles > 0) {
+    qd.copy(Q0, qstart, wave);
+    od.copy(O0, qstart, wave);
+    stats(qstart, L0, D0);
+    __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
+    __syncthreads();
+  }
+  constexpr std::true_type masked{};
+  constexpr std::false_type open{};
+  if (MASK || ntiles <= 2) {
+    run(masked, 0, ntiles);
+  } else {
+    const int lead = CAUSAL ? 2 : 0, end = t_q % TILE ? ntiles - 1 : ntiles;
+    if (lead) run(masked, 0, lead);
+    run(open, lead, end);
+    if (end < ntiles) {
+      if (end & 1) step(masked, end, Q1, O1, L1, D1, Q0, O0, L0, D0);
+      else step(masked, end, Q0, O0, L0, D0, Q1, O1, L1, D1);
+    }
+  }
+  store_transposed<T, D>(dk + b * (int64_t)t_k * D, gk, key, t_k, 1.f);
+  store_transposed<T, D>(dv + b * (int64_t)t_k * D, gv, key, t_k, 1.f);
+}
+
 // ---------------------------------------------------------------------------------------------
 
 // Resident 32-row tiles per wave for each pass and head dim: 2 (each LDS operand read feeds two
@@ -686,6 +942,10 @@ int launch_nt(const SdpaArgs& a) {
     hipLaunchKernelGGL((sdpa_bwd_q_mfma<T, D, NT, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q,
                        (const u16*)a.k, (const u16*)a.v, (const u16*)a.dout, (const float*)a.lse, (const float*)a.delta,
                        mask, (u16*)a.out0, a.batch, (int)a.t_q, (int)a.t_k, scale);
+  } else if constexpr (D == 128) {
+    hipLaunchKernelGGL((sdpa_bwd_kv_dma<T, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q, (const u16*)a.k,
+                       (const u16*)a.v, (const u16*)a.dout, (const float*)a.lse, (const float*)a.delta, mask,
+                       (u16*)a.out0, (u16*)a.out1, a.batch, (int)a.t_q, (int)a.t_k, scale);
   } else {
     hipLaunchKernelGGL((sdpa_bwd_kv_mfma<T, D, NT, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q,
                        (const u16*)a.k, (const u16*)a.v, (const u16*)a.dout, (const float*)a.lse, (const float*)a.delta,
@@ -726,9 +986,9 @@ bool mfma_supports(int dtype, int64_t hd, int64_t hd_v) {
 }
 
 bool mfma_fits(int64_t t_q, int64_t t_k, int64_t hd) {
-  // per-head offsets are 32-bit inside the kernels
+  // per-head byte offsets are 32-bit inside the kernels (buffer resources included)
   const int64_t limit = ((int64_t)1 << 31) - 1;
-  return t_q * hd < limit && t_k * hd < limit;
+  return t_q * hd * 2 < limit && t_k * hd * 2 < limit;
 }
 
 int launch_sdpa_mfma(SdpaPass pass, const SdpaArgs& a) {
