@@ -632,7 +632,7 @@ def main() -> int:
     KERNEL_SYMBOL = {
         "sdpa": "sdpa_fwd_mfma<BF16,128,1,true,false>",
         "sdpa_bwd_q": "sdpa_bwd_q_mfma<BF16,128,1,true,false>",
-        "sdpa_bwd_kv": "sdpa_bwd_kv_mfma<BF16,128,1,true,false>",
+        "sdpa_bwd_kv": "sdpa_bwd_kv_dma<BF16,true,false>",
     }
     dom = int(np.argmax(per))
     achieved = kernel_flops[names[dom]] / (per[dom] * 1e-3)
