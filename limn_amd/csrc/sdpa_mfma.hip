@@ -153,13 +153,17 @@ struct Stage {
   static constexpr int SLOTS = (2 * PER_TILE + THREADS - 1) / THREADS;
   u16x8 r[SLOTS][4];
 
+  static_assert(PER_TILE % 64 == 0, "a wave's blocks come from one matrix");
+
   // rows [row0, row0 + TILE) of both matrices; rows past their end read as zeros
   __device__ __forceinline__ void load(const Rows& m0, const Rows& m1, int row0) {
 #pragma unroll
     for (int s = 0; s < SLOTS; s++) {
       const int idx = threadIdx.x + s * THREADS;
       if (idx < 2 * PER_TILE) {
-        const int which = idx / PER_TILE, w = idx - which * PER_TILE;
+        // a whole wave reads one matrix: saying so keeps its buffer resource in scalar
+        // registers (a per-lane choice would wrap every load in a loop over distinct resources)
+        const int which = __builtin_amdgcn_readfirstlane(idx / PER_TILE), w = idx - which * PER_TILE;
         const int col = w % COLS, grp = w / COLS;
         const Rows& m = which ? m1 : m0;
 #pragma unroll
