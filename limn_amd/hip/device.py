@@ -32,6 +32,21 @@ from limn_amd.schedule import realized
 SDPA, SDPA_BWD_Q, SDPA_BWD_KV = "sdpa", "sdpa_bwd_q", "sdpa_bwd_kv"
 
 
+# One workgroup per table entry (value, target, bytes <= 64 KiB, 16-byte aligned starts): 16-byte
+# copies, then the entry's tail byte by byte.
+COMMIT_SOURCE = r"""
+extern "C" __global__ void limn_commit_batch(const long long* __restrict__ table, long long entries) {
+  const long long e = blockIdx.x;
+  if (e >= entries) return;
+  const char* src = (const char*)table[3 * e];
+  char* dst = (char*)table[3 * e + 1];
+  const long long n = table[3 * e + 2], whole = n / 16;
+  for (long long i = threadIdx.x; i < whole; i += blockDim.x) ((uint4*)dst)[i] = ((const uint4*)src)[i];
+  for (long long i = whole * 16 + threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
+}
+"""
+
+
 class HipBuffer:
     """Device bytes; the pointer returns to its device's pool when the last reference drops."""
 
@@ -70,6 +85,10 @@ class HipDevice(CompiledDevice):
         self.clock_khz = clock.value
         self.global_mem = mem.value
         self.pool: dict[int, list[int]] = {}
+        # ASSIGN commits to device buffers, queued until finish() copies them in one launch
+        self._commits: list[tuple[Buffer, Buffer]] = []
+        self._committed: list[tuple[Buffer, Buffer]] = []  # launched, kept alive until the barrier
+        self._commit_table: tuple[int, int, Buffer] | None = None  # (pinned host ptr, entries, device copy)
         self.custom[SDPA] = self._sdpa_runner
         self.custom[SDPA_BWD_Q] = self._sdpa_runner
         self.custom[SDPA_BWD_KV] = self._sdpa_runner
@@ -126,13 +145,53 @@ class HipDevice(CompiledDevice):
         return buf
 
     def commit(self, target: Buffer, value: Buffer) -> None:
+        """A device target's copy is queued: finish() runs every commit of the batch as one kernel
+        (a training step commits hundreds of parameters and moments, one launch each otherwise;
+        reference limn/backend_cuda.py:343-347 issues a cuMemcpyDtoD per commit). A host target is
+        written at once."""
         if isinstance(target, np.ndarray):
             check(self.api.hipMemcpy(target.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(value.ptr), target.nbytes, DEVICE_TO_HOST), "committing an assign to host")
-        else:
-            check(self.api.hipMemcpyAsync(ctypes.c_void_p(target.ptr), ctypes.c_void_p(value.ptr), value.nbytes, DEVICE_TO_DEVICE, None), "committing an assign")
+            return
+        if any(t.ptr == target.ptr for t, _ in self._commits):
+            self._flush_commits()  # a second commit to one target in a batch: the later one wins
+        self._commits.append((target, value))
+
+    COMMIT_CHUNK = 1 << 16  # bytes per workgroup of the commit kernel
+
+    def _flush_commits(self) -> None:
+        if not self._commits:
+            return
+        entries = []
+        for target, value in self._commits:
+            for off in range(0, value.nbytes, self.COMMIT_CHUNK):
+                entries.append((value.ptr + off, target.ptr + off, min(self.COMMIT_CHUNK, value.nbytes - off)))
+        if self._committed:
+            # the pinned table of an earlier launch in this batch may not have been read yet
+            check(self.api.hipStreamSynchronize(None), "waiting for a commit table")
+        table = np.array(entries, dtype=np.int64)
+        host, cap, dev_table = self._commit_table or (0, 0, None)
+        if cap < len(entries):
+            if host:
+                check(self.api.hipStreamSynchronize(None), "waiting for a commit table")
+                self.api.hipHostFree(ctypes.c_void_p(host))
+            cap = max(len(entries), 2 * cap, 1024)
+            ptr = ctypes.c_void_p()
+            check(self.api.hipHostMalloc(ctypes.byref(ptr), cap * 24, 0), "allocating a pinned commit table")
+            host, dev_table = ptr.value, self._alloc(cap * 24)
+            self._commit_table = (host, cap, dev_table)
+        ctypes.memmove(host, table.ctypes.data, table.nbytes)
+        check(self.api.hipMemcpyAsync(ctypes.c_void_p(dev_table.ptr), ctypes.c_void_p(host), table.nbytes, HOST_TO_DEVICE, None), "uploading a commit table")
+        fn = runtime.load_functions(COMMIT_SOURCE, ["limn_commit_batch"])["limn_commit_batch"]
+        args = (ctypes.c_void_p * 2)(ctypes.c_void_p(dev_table.ptr), ctypes.c_void_p(len(entries)))
+        params = (ctypes.c_void_p * 2)(*[ctypes.addressof(args) + k * ctypes.sizeof(ctypes.c_void_p) for k in range(2)])
+        check(self.api.hipModuleLaunchKernel(fn, len(entries), 1, 1, 256, 1, 1, 0, None, params, None), "launching the commits")
+        self._committed += self._commits
+        self._commits = []
 
     def finish(self) -> None:
+        self._flush_commits()
         check(self.api.hipDeviceSynchronize(), "waiting for the batch")
+        self._committed = []
 
     def plan_of(self, order: list[Node], position: dict[Node, int], sinks: list[Node]):
         """The executor's plan_of, with the buffers that must hold their values recorded for

@@ -44,6 +44,8 @@ _HIP = {
     "hipMemcpy": (c_int, [c_void_p, c_void_p, c_size_t, c_int]),
     "hipMemcpyAsync": (c_int, [c_void_p, c_void_p, c_size_t, c_int, c_void_p]),
     "hipMemsetAsync": (c_int, [c_void_p, c_int, c_size_t, c_void_p]),
+    "hipHostMalloc": (c_int, [P(c_void_p), c_size_t, c_uint]),
+    "hipHostFree": (c_int, [c_void_p]),
     "hipMemGetInfo": (c_int, [P(c_size_t), P(c_size_t)]),
     "hipDeviceSynchronize": (c_int, []),
     "hipStreamSynchronize": (c_int, [c_void_p]),

@@ -166,6 +166,55 @@ def test_assign_is_deferred_until_every_sink_is_computed(hipdev):
     np.testing.assert_array_equal(hipdev.copyout(bufs[1]).view(np.float32), np.full(4, 2.0, np.float32))
 
 
+def test_commits_of_a_batch_run_as_one_copy(hipdev):
+    """Device-target commits are queued and copied in finish(): sizes that leave byte tails, a
+    copy longer than one 64 KiB chunk, several dtypes in one batch, and a target committed twice
+    (the later value wins)."""
+    sizes = [1, 7, 16, 33, 65536, 65536 * 3 + 5, 1 << 20]
+    targets, values, want = [], [], []
+    for n in sizes:
+        t, v = hipdev.alloc(n), hipdev.alloc(n)
+        data = rng.integers(0, 256, size=n, dtype=np.uint8)
+        hipdev.copyin(v, data)
+        targets.append(t)
+        values.append(v)
+        want.append(data)
+    for t, v in zip(targets, values):
+        hipdev.commit(t, v)
+    again = hipdev.alloc(sizes[3])
+    later = rng.integers(0, 256, size=sizes[3], dtype=np.uint8)
+    hipdev.copyin(again, later)
+    hipdev.commit(targets[3], again)
+    want[3] = later
+    hipdev.finish()
+    for t, w in zip(targets, want):
+        np.testing.assert_array_equal(hipdev.copyout(t), w)
+
+
+def test_assigns_commit_after_every_call(hipdev):
+    """A training-style batch: three tensors assigned from expressions that read all three; every
+    read sees the old values (reference tests/test_compiled_devices.py:73-98), and the commits land
+    through the batched copy."""
+    limn_device.active_device = hipdev
+    a = Tensor(np.arange(1000, dtype=np.float32))
+    b = Tensor(np.arange(1000, dtype=np.float32) * 2.0, dtype=bfloat16)
+    c = Tensor(np.full(70001, 3.0, dtype=np.float32))
+    from limn_amd.dtypes import bf16_bits, bf16_values
+
+    a_old = np.arange(1000, dtype=np.float32)
+    b_old = bf16_values(bf16_bits(np.arange(1000, dtype=np.float32) * 2.0)).astype(np.float32)  # b is stored as bf16
+    na, nb, nc = a + b.cast(float32), b * 2.0, c + a.sum()
+    a.assign(na)
+    b.assign(nb)
+    c.assign(nc)
+    got = [hipdev.copyout(buf) for buf in hipdev.execute([a.node, b.node, c.node])]
+    from limn_amd.dtypes import from_storage
+
+    np.testing.assert_allclose(got[0].view(np.float32), a_old + b_old)
+    np.testing.assert_allclose(from_storage(got[1], bfloat16, (1000,)).astype(np.float32), b_old * 2.0, rtol=1e-2)
+    np.testing.assert_allclose(got[2].view(np.float32), np.full(70001, 3.0 + a_old.sum(), np.float32), rtol=1e-5)
+
+
 def test_one_plan_for_a_repeated_graph(hipdev):
     before = len(hipdev.plans)
     for _ in range(3):
