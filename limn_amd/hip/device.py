@@ -87,6 +87,7 @@ class HipDevice(CompiledDevice):
         self.pool: dict[int, list[int]] = {}
         # ASSIGN commits to device buffers, queued until finish() copies them in one launch
         self._commits: list[tuple[Buffer, Buffer]] = []
+        self._commit_targets: set[int] = set()
         self._committed: list[tuple[Buffer, Buffer]] = []  # launched, kept alive until the barrier
         self._commit_table: tuple[int, int, Buffer] | None = None  # (pinned host ptr, entries, device copy)
         self.custom[SDPA] = self._sdpa_runner
@@ -152,9 +153,10 @@ class HipDevice(CompiledDevice):
         if isinstance(target, np.ndarray):
             check(self.api.hipMemcpy(target.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(value.ptr), target.nbytes, DEVICE_TO_HOST), "committing an assign to host")
             return
-        if any(t.ptr == target.ptr for t, _ in self._commits):
+        if target.ptr in self._commit_targets:
             self._flush_commits()  # a second commit to one target in a batch: the later one wins
         self._commits.append((target, value))
+        self._commit_targets.add(target.ptr)
 
     COMMIT_CHUNK = 1 << 16  # bytes per workgroup of the commit kernel
 
@@ -187,6 +189,7 @@ class HipDevice(CompiledDevice):
         check(self.api.hipModuleLaunchKernel(fn, len(entries), 1, 1, 256, 1, 1, 0, None, params, None), "launching the commits")
         self._committed += self._commits
         self._commits = []
+        self._commit_targets = set()
 
     def finish(self) -> None:
         self._flush_commits()
