@@ -23,8 +23,10 @@ one-thread-per-cell launch):
 - few cells over a long reduce (the reference's split reduce, limn/cuda_emit.py:134-149):
   PARTS workgroups per cell write partials to a scratch buffer, and a second kernel folds each
   cell's partials in index order;
-- SCATTER adds with hardware atomics (float32, float64, int32); like the reference's GPU
-  device, the half widths and narrow ints are refused.
+- a float SCATTER (float32, float64) gives np.add.at's bits: a tiled sort of the occurrences by
+  row, then a workgroup per (row, 64 columns) adds that row's values in occurrence order
+  (`plan_scatter`). An int32 SCATTER adds with hardware atomics, which is exact in any order.
+  Like the reference's GPU device, the half widths and narrow ints are refused.
 """
 
 from __future__ import annotations
@@ -285,7 +287,7 @@ class Launch:
     name: str
     grid: int
     block: int
-    args: str  # "io" (inputs then out), "io_scratch" (inputs then scratch), "scratch_out"
+    args: str  # "io" (inputs then out), "io_scratch" (inputs then scratch), "io_scratch_out", "scratch_out"
 
 
 @dataclass
@@ -452,12 +454,219 @@ def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned
     if write.opcode is Opcode.SCATTER:
         if out_dtype not in (float32, float64, int32):
             raise NotImplementedError(f"the hip device cannot scatter {out_dtype}; cast the table to float32 or int32")
+        if out_dtype is not int32:
+            return plan_scatter(nest, shape, bufs)
         lines.append(f"      atomicAdd(&{buf}[{render_index(index, True)}], ({STORE_T[out_dtype]}){write.srcs[0]});")
     else:
         lines.append(f"      {buf}[{render_index(index, wide)}] = {store_expr(out_dtype, write.srcs[0])};")
     lines += ["    }", "  }", "}"]
     grid = max(1, min(-(-groups // THREADS), 1 << 20))
     return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")])
+
+
+SORT_TILE_LIMITS = ((1 << 16, 256), (1 << 20, 1024))  # occurrences -> occurrences per sorted tile
+SORT_TILE_MAX = 4096
+LIST_CAP = 1024  # a row's occurrences gathered in LDS per pass of the accumulating kernel
+
+
+def _reads(instr: Instr) -> set[str]:
+    """Every name an instruction reads: its operands, the variables of its index and of its
+    bound checks."""
+    names = set(instr.srcs)
+    if instr.opcode in (Opcode.LOAD, Opcode.GATHER):
+        names |= {v for v, _ in instr.arg[1].terms}
+    if instr.opcode is Opcode.LOAD:
+        names |= {b[0] for b in instr.arg[2].bounds}
+    if instr.opcode is Opcode.CONST:
+        names |= {b[0] for b in instr.arg[1].bounds}
+    return names
+
+
+def _needed(body: list[Instr], roots: set[str]) -> list[Instr]:
+    """The instructions of `body` that `roots` depend on, in body order."""
+    by_dest = {i.dest: i for i in body}
+    need: set[str] = set()
+    stack = list(roots)
+    while stack:
+        name = stack.pop()
+        if name in need or name not in by_dest:
+            continue
+        need.add(name)
+        stack.extend(_reads(by_dest[name]))
+    return [i for i in body if i.dest in need]
+
+
+def plan_scatter(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
+    """A float SCATTER whose totals equal np.add.at's bit for bit: every table row is the sum of
+    its values in occurrence order, added one at a time onto 0 (reference limn/device.py:153-158
+    is the rule; its GPU device adds with atomics in whatever order they land,
+    limn/cuda_emit.py:694-703).
+
+    The nest loops over the values, (occurrences..., column); each occurrence's row comes from
+    the index instructions of the body, which read only the occurrence variables. Two kernels:
+
+    - `<name>_sort`: a workgroup per tile of consecutive occurrences computes each one's row and
+      sorts the tile in LDS by (row, occurrence), a bitonic network over unique 64-bit keys, so
+      each row's occurrences in the tile come out contiguous and ascending. Rows outside the
+      table (after the wrap of negatives, as numpy indexes) sort last and are never read;
+    - `<name>`: a one-wave workgroup per (row, block of 64 columns) finds the row's run in 64
+      tiles at a time by binary search (a lane per tile), gathers those runs into one list in
+      LDS in tile order, which is occurrence order, then walks the list evaluating the value
+      instructions at (occurrence, column) and adding them into one register per lane, 16
+      occurrences' loads in flight at a time; the total is stored to every row, the empty
+      ones as 0.
+
+    FMA contraction is off in the accumulating kernel so a value computed by a product is
+    rounded before it is added, as numpy rounds it."""
+    out_dtype = nest.kernel.target.dtype
+    table = nest.kernel.target.shape
+    if len(table) != 2:
+        raise NotImplementedError(f"the hip device scatters into 2-D tables, not {table}")
+    rows_n, cols = table
+    lead = [(f"i{d}", e) for d, e in enumerate(nest.space[:-1])]
+    col_var = f"i{len(nest.space) - 1}"
+    if nest.space[-1] != cols:
+        raise NotImplementedError(f"scatter values {nest.space} do not end in the table's {cols} columns")
+    occurrences = math.prod(e for _, e in lead)
+    if occurrences >= (1 << 31):
+        raise NotImplementedError(f"the hip device scatters fewer than 2^31 rows, not {occurrences}")
+    write = shape.write
+    index = write.arg[1]
+    loop_names = {v for v, _ in shape.outer}
+    row_terms = [(v, c) for v, c in index.terms if v not in loop_names]
+    if len(row_terms) > 1:
+        raise NotImplementedError(f"a scatter row index with several computed terms: {index}")
+    row_name = row_terms[0][0] if row_terms else None
+    key_body = _needed(shape.body, {row_name}) if row_name else []
+    if any(col_var in _reads(i) for i in key_body):
+        raise NotImplementedError("a scatter row index that depends on the column")
+    value_body = _needed(shape.body, {write.srcs[0]})
+    acc_t = STORE_T[out_dtype]
+    wide = bufs.wide_index
+    tile = next((t for limit, t in SORT_TILE_LIMITS if occurrences <= limit), SORT_TILE_MAX)
+    tiles = max(1, -(-occurrences // tile))
+    block = 64  # one wave: the scan and the tile search below are lane-wide
+    col_blocks = max(1, -(-cols // block))
+    params = [f"const {STORE_T[n.dtype]}* __restrict__ in{k}" for k, n in enumerate(nest.kernel.inputs)]
+
+    per = tile // THREADS  # occurrences per thread, held in registers as thread * per + e
+    sort = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {nest.name}_sort({", ".join(params + ["unsigned long long* __restrict__ runs"])}) {{']
+    sort.append(f"  __shared__ unsigned long long s_[{tile}];")
+    sort.append(f"  const i64 base_ = (i64)blockIdx.x * {tile};")
+    sort.append("  const int th_ = threadIdx.x;")
+    sort.append(f"  unsigned long long x_[{per}];")
+    sort.append("#pragma unroll")
+    sort.append(f"  for (int e_ = 0; e_ < {per}; e_++) {{")
+    sort.append(f"    const i64 o_ = base_ + th_ * {per} + e_;")
+    sort.append("    unsigned long long key_ = ~0ull;")
+    sort.append(f"    if (o_ < {occurrences}LL) {{")
+    sort += decode(lead, "o_", "      ", True)
+    sort += ["      " + value_line(i, bufs) for i in key_body]
+    sort.append(f"      long long row_ = {f'(long long){row_name}' if row_name else '0'};")
+    sort.append(f"      if (row_ < 0) row_ += {rows_n}LL;")
+    sort.append(f"      if (row_ < 0 || row_ >= {rows_n}LL) row_ = {rows_n}LL;")
+    sort.append("      key_ = ((unsigned long long)row_ << 32) | (unsigned long long)o_;")
+    sort.append("    }")
+    sort.append("    x_[e_] = key_;")
+    sort.append("  }")
+    # bitonic network: stride j pairs element i with i ^ j; the pair runs ascending when
+    # (i & k) == 0. Strides of a wave's reach or more go through LDS, shorter ones of at least
+    # `per` through lane shuffles, the rest inside a thread's registers.
+    sort.append(f"  for (int k_ = 2; k_ <= {tile}; k_ <<= 1) {{")
+    sort.append(f"    for (int j_ = k_ >> 1; j_ >= {per}; j_ >>= 1) {{")
+    sort.append(f"      if (j_ >= {64 * per}) {{")
+    sort.append("#pragma unroll")
+    sort.append(f"        for (int e_ = 0; e_ < {per}; e_++) s_[th_ * {per} + e_] = x_[e_];")
+    sort.append("        __syncthreads();")
+    sort.append("#pragma unroll")
+    sort.append(f"        for (int e_ = 0; e_ < {per}; e_++) {{")
+    sort.append(f"          const int i_ = th_ * {per} + e_;")
+    sort.append("          const unsigned long long y_ = s_[i_ ^ j_];")
+    sort.append("          const bool low_ = ((i_ & j_) == 0) == ((i_ & k_) == 0);")
+    sort.append("          x_[e_] = low_ ? (x_[e_] < y_ ? x_[e_] : y_) : (x_[e_] < y_ ? y_ : x_[e_]);")
+    sort.append("        }")
+    sort.append("        __syncthreads();")
+    sort.append("      } else {")
+    sort.append("#pragma unroll")
+    sort.append(f"        for (int e_ = 0; e_ < {per}; e_++) {{")
+    sort.append(f"          const int i_ = th_ * {per} + e_;")
+    sort.append(f"          const unsigned long long y_ = __shfl_xor(x_[e_], j_ / {per});")
+    sort.append("          const bool low_ = ((i_ & j_) == 0) == ((i_ & k_) == 0);")
+    sort.append("          x_[e_] = low_ ? (x_[e_] < y_ ? x_[e_] : y_) : (x_[e_] < y_ ? y_ : x_[e_]);")
+    sort.append("        }")
+    sort.append("      }")
+    sort.append("    }")
+    j = per // 2
+    while j > 0:
+        sort.append(f"    if ({j} < k_) {{")
+        for e in range(per):
+            if e & j:
+                continue
+            sort.append(f"      if ((x_[{e}] > x_[{e | j}]) == (((th_ * {per} + {e}) & k_) == 0)) {{ const unsigned long long y_ = x_[{e}]; x_[{e}] = x_[{e | j}]; x_[{e | j}] = y_; }}")
+        sort.append("    }")
+        j //= 2
+    sort.append("  }")
+    sort.append("#pragma unroll")
+    sort.append(f"  for (int e_ = 0; e_ < {per}; e_++) runs[base_ + th_ * {per} + e_] = x_[e_];")
+    sort.append("}")
+
+    acc = [f'extern "C" __global__ __launch_bounds__({block}) void {nest.name}({", ".join(params + ["const unsigned long long* __restrict__ runs", f"{acc_t}* __restrict__ out"])}) {{']
+    acc.append("#pragma clang fp contract(off)")
+    acc.append("  __shared__ int lo_[64], start_[64];")
+    acc.append(f"  __shared__ unsigned list_[{LIST_CAP}];")
+    acc.append("  const int lane_ = threadIdx.x;")
+    work = rows_n * col_blocks
+    acc.append(f"  for (i64 w_ = blockIdx.x; w_ < {work}LL; w_ += gridDim.x) {{")
+    acc.append(f"  const int r_ = (int)(w_ / {col_blocks});")
+    acc.append(f"  const int c_ = (int)(w_ % {col_blocks}) * {block} + threadIdx.x;")
+    acc.append(f"  const int {col_var} = c_ < {cols} ? c_ : {cols - 1};  // past the last column: read a valid one, store nothing")
+    acc.append(f"  {acc_t} acc_ = 0;")
+    acc.append(f"  for (int t0_ = 0; t0_ < {tiles}; t0_ += 64) {{")
+    acc.append("    int a_ = 0, len_ = 0;")
+    acc.append(f"    if (t0_ + lane_ < {tiles}) {{")
+    acc.append(f"      const unsigned long long* run_ = runs + (i64)(t0_ + lane_) * {tile};")
+    acc.append("      const unsigned long long first_ = (unsigned long long)r_ << 32, past_ = (unsigned long long)(r_ + 1) << 32;")
+    acc.append(f"      int n_ = {tile};")
+    acc.append("      while (n_ > 0) { const int h_ = n_ >> 1; if (run_[a_ + h_] < first_) { a_ += h_ + 1; n_ -= h_ + 1; } else n_ = h_; }")
+    acc.append(f"      int b_ = a_; n_ = {tile} - a_;")
+    acc.append("      while (n_ > 0) { const int h_ = n_ >> 1; if (run_[b_ + h_] < past_) { b_ += h_ + 1; n_ -= h_ + 1; } else n_ = h_; }")
+    acc.append("      len_ = b_ - a_;")
+    acc.append("    }")
+    acc.append("    int incl_ = len_;  // where each tile's run starts in this row's list: a scan over the wave")
+    acc.append("    for (int d_ = 1; d_ < 64; d_ <<= 1) { const int y_ = __shfl_up(incl_, d_); if (lane_ >= d_) incl_ += y_; }")
+    acc.append("    const int total_ = __shfl(incl_, 63);")
+    acc.append("    __syncthreads();  // the previous readers of lo_, start_ and list_ are done")
+    acc.append("    lo_[lane_] = a_; start_[lane_] = incl_ - len_;")
+    acc.append("    __syncthreads();")
+    acc.append(f"    for (int base_ = 0; base_ < total_; base_ += {LIST_CAP}) {{")
+    acc.append(f"      const int n_ = total_ - base_ < {LIST_CAP} ? total_ - base_ : {LIST_CAP};")
+    acc.append("      if (base_) __syncthreads();")
+    acc.append("      for (int p_ = lane_; p_ < n_; p_ += 64) {")
+    acc.append("        const int q_ = base_ + p_;")
+    acc.append("        int t_ = 0;  // the last tile whose run starts at or before q_")
+    acc.append("        for (int s_ = 32; s_ > 0; s_ >>= 1) if (start_[t_ + s_] <= q_) t_ += s_;")
+    acc.append(f"        list_[p_] = (unsigned)runs[(i64)(t0_ + t_) * {tile} + lo_[t_] + (q_ - start_[t_])];")
+    acc.append("      }")
+    acc.append("      __syncthreads();")
+    acc.append("#pragma unroll 16")
+    acc.append("      for (int j_ = 0; j_ < n_; j_++) {")
+    acc.append("        const i64 o_ = (i64)list_[j_];")
+    acc += decode(lead, "o_", "        ", True)
+    acc += ["        " + value_line(i, bufs) for i in value_body]
+    acc.append(f"        acc_ += ({acc_t}){write.srcs[0]};")
+    acc.append("      }")
+    acc.append("    }")
+    acc.append("  }")
+    acc.append(f"  if (c_ < {cols}) {{")
+    if row_name:
+        acc.append(f"    const int {row_name} = r_;")
+    acc.append(f"    out[{render_index(index, True)}] = acc_;")
+    acc.append("  }")
+    acc.append("  }")
+    acc.append("}")
+    launches = [Launch(nest.name + "_sort", tiles, THREADS, "io_scratch"), Launch(nest.name, max(1, min(work, 1 << 20)), block, "io_scratch_out")]
+    return Planned("\n".join(sort + acc), launches, scratch_bytes=tiles * tile * 8,
+                   notes={"ordered scatter": True, "tile": tile, "tiles": tiles})
 
 
 def _fold(op: Op, acc: str, x: str) -> str:
@@ -791,7 +1000,7 @@ def nest_runners(dev, nests: list[LoopNest]):
         nin = len(nest.kernel.inputs)
         launchers = []
         for launch in plan.launches:
-            count = nin + 1 if launch.args in ("io", "io_scratch") else 2
+            count = {"io": nin + 1, "io_scratch": nin + 1, "io_scratch_out": nin + 2}.get(launch.args, 2)
             launchers.append((launch.args, _launcher(dev, functions[launch.name], launch, count - 1)))
         runners.append(_make_runner(dev, launchers, plan.scratch_bytes))
     return runners
@@ -861,6 +1070,8 @@ def _make_runner(dev, launchers, scratch_bytes: int):
                 launch(ins + [outs[0].ptr])
             elif kind == "io_scratch":
                 launch(ins + [held[0].ptr])
+            elif kind == "io_scratch_out":
+                launch(ins + [held[0].ptr, outs[0].ptr])
             else:
                 launch([held[0].ptr, outs[0].ptr])
 

@@ -32,11 +32,12 @@ GRAPHS = {
 }
 
 
-def check(dev, t, rtol: float = 1e-5, atol: float = 1e-5, exact: bool = False, worst: float | None = None) -> None:
+def check(dev, t, rtol: float = 1e-5, atol: float = 1e-5, exact: bool = False, worst: float | None = None, bitwise: bool = False) -> None:
     """Realize `t` on `dev` first, then on the numpy oracle (which retires the node), and diff
     (reference tests/conftest.py:52-69). Half widths compare widened to float32. With `worst`,
     the bound is on max|got - want| / max(1, max|want|) instead (reference limn/sdpa.py:251-259):
-    for sums whose terms cancel, where no per-element relative bound holds across orders."""
+    for sums whose terms cancel, where no per-element relative bound holds across orders. With
+    `bitwise`, the stored bytes must be identical (a -0.0 or a NaN payload counts)."""
     got = from_storage(dev.copyout(dev.execute([t.node])[0]), t.dtype, t.shape)
     saved = limn_device.active_device
     limn_device.active_device = NumpyDevice()
@@ -44,6 +45,13 @@ def check(dev, t, rtol: float = 1e-5, atol: float = 1e-5, exact: bool = False, w
         want = t.numpy()
     finally:
         limn_device.active_device = saved
+    if bitwise:
+        assert got.dtype == want.dtype and got.shape == want.shape, (got.dtype, want.dtype, got.shape, want.shape)
+        g, w = np.ascontiguousarray(got).reshape(-1), np.ascontiguousarray(want).reshape(-1)
+        differ = np.any(g.view(np.uint8).reshape(g.size, -1) != w.view(np.uint8).reshape(w.size, -1), axis=1)
+        bad = np.flatnonzero(differ)
+        assert bad.size == 0, f"{bad.size} of {g.size} values differ in their bits; first at {bad[:5]}: got {g[bad[:5]]}, want {w[bad[:5]]}"
+        return
     if exact:
         np.testing.assert_array_equal(got, want)
         return

@@ -79,14 +79,64 @@ def test_gather_rows(hipdev):
     check(hipdev, table[idx], exact=True)
 
 
+def order_sensitive(*shape: int) -> np.ndarray:
+    """Values whose float sum depends on the order of the adds: large terms that cancel among
+    small ones, so a reordering moves the small ones' rounding."""
+    big = rng.choice(np.array([3e7, -3e7, 1e8, -1e8], np.float32), size=shape)
+    small = rng.uniform(-4, 4, shape).astype(np.float32)
+    return np.where(rng.random(shape) < 0.3, big, small).astype(np.float32)
+
+
 def test_scatter_with_repeats(hipdev):
-    """512 values land on one row: atomics collide, the total still matches (reference
-    tests/test_backend_cuda.py:125-131)."""
-    values = Tensor(randf(512, 8))
-    idx = Tensor(np.zeros(512, dtype=np.int32))
+    """512 values land on one row (reference tests/test_backend_cuda.py:125-131 allows 1e-4 for
+    its atomics); here the total is np.add.at's, bit for bit."""
     from limn_amd.tensor import scatter_rows
 
-    check(hipdev, scatter_rows(values, idx, (4, 8)), rtol=1e-4, atol=1e-4)
+    values = order_sensitive(512, 8)
+    idx = np.zeros(512, dtype=np.int32)
+    forward, backward = np.zeros((4, 8), np.float32), np.zeros((4, 8), np.float32)
+    np.add.at(forward, idx, values)
+    np.add.at(backward, idx[::-1], values[::-1])
+    assert np.any(forward != backward), "the values must be order-sensitive for this test to mean anything"
+    check(hipdev, scatter_rows(Tensor(values), Tensor(idx), (4, 8)), bitwise=True)
+
+
+@pytest.mark.parametrize(
+    "occurrences,rows,cols",
+    [((7, 9), 10, 16), ((3000,), 5, 100), ((70000,), 300, 3), ((300000,), 40, 2), ((32, 512), 256, 512), ((5,), 3, 1), ((4,), 1000, 8)],
+    ids=["small", "ragged-columns", "tiles-of-4096", "more-tiles-than-a-wave", "gpt-token-table", "one-column", "mostly-empty-rows"],
+)
+def test_float_scatter_is_occurrence_ordered(hipdev, occurrences, rows, cols):
+    """Float SCATTER equals np.add.at bit for bit (the oracle's rule, reference
+    limn/device.py:153-158): each row adds its values in occurrence order onto 0. Negative
+    indices count from the end as numpy's do; some rows get nothing and stay 0."""
+    from limn_amd.tensor import scatter_rows
+
+    values = order_sensitive(*occurrences, cols)
+    idx = rng.integers(-rows, rows, size=occurrences).astype(np.int32)
+    check(hipdev, scatter_rows(Tensor(values), Tensor(idx), (rows, cols)), bitwise=True)
+
+
+def test_float64_scatter_and_computed_values_are_ordered(hipdev):
+    """A float64 table, and values computed in the nest (a product then a sum, which must not be
+    fused into one rounding)."""
+    from limn_amd.tensor import scatter_rows
+
+    idx = Tensor(rng.integers(0, 7, size=(400,)).astype(np.int32))
+    v64 = Tensor(order_sensitive(400, 6).astype(np.float64) * 1.1, dtype=float64)
+    check(hipdev, scatter_rows(v64, idx, (7, 6)), bitwise=True)
+    v = Tensor(order_sensitive(400, 6))
+    check(hipdev, scatter_rows(v * 3.3 + 0.7, idx, (7, 6)), bitwise=True)
+
+
+def test_scatter_grid_covers_more_rows_than_one_launch(hipdev):
+    """A table of more (row, column block) items than the accumulating launch has workgroups."""
+    from limn_amd.tensor import scatter_rows
+
+    rows = (1 << 20) + 77
+    idx = Tensor(rng.integers(0, rows, size=(5000,)).astype(np.int32))
+    values = Tensor(order_sensitive(5000, 1))
+    check(hipdev, scatter_rows(values, idx, (rows, 1)), bitwise=True)
 
 
 def test_scatter_int32_is_exact(hipdev):
@@ -110,7 +160,7 @@ def test_gather_backward_scatters(hipdev):
     table = Tensor(randf(10, 4), requires_grad=True)
     idx = Tensor(rng.integers(0, 10, size=(6, 3)).astype(np.int32))
     (g,) = grad((table[idx] * Tensor(randf(6, 3, 4))).sum(), [table])
-    check(hipdev, g, rtol=1e-5, atol=1e-5)
+    check(hipdev, g, bitwise=True)
 
 
 @pytest.mark.parametrize("dtype,tol", [(float64, 1e-12), (float16, 2e-3), (bfloat16, 1e-2)], ids=str)
