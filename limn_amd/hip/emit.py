@@ -144,10 +144,30 @@ def arith(op: Op, srcs: tuple[str, ...], dtype: DType) -> str:
 
 @dataclass
 class Buffers:
-    """Element types of a nest's buffers by name (in0.., out) and whether 64-bit indexing is needed."""
+    """Element types of a nest's buffers by name (in0.., out) and whether 64-bit indexing is needed.
+    `inline` maps an input's name to the producer evaluated in its place (see `inline_producers`),
+    whose own inputs are the kernel's `extra` parameters, after in0.. and before out."""
 
     dtypes: dict[str, DType]
     wide_index: bool
+    inline: dict[str, "Inlined"] = field(default_factory=dict)
+    extra: list[str] = field(default_factory=list)
+
+
+@dataclass(frozen=True)
+class Inlined:
+    """A small elementwise nest evaluated where a reader loads its output: its body with every
+    name prefixed, its loop variables over its output shape, and the rounding of its store."""
+
+    space: tuple[tuple[str, int], ...]
+    body: tuple[Instr, ...]
+    result: str
+    dtype: DType
+
+
+def input_params(nest: LoopNest, bufs: Buffers) -> list[str]:
+    params = [f"const {STORE_T[n.dtype]}* __restrict__ in{k}" for k, n in enumerate(nest.kernel.inputs)]
+    return params + [f"const {STORE_T[bufs.dtypes[name]]}* __restrict__ {name}" for name in bufs.extra]
 
 
 def render_index(index: Index, wide: bool) -> str:
@@ -171,6 +191,8 @@ def value_line(instr: Instr, bufs: Buffers) -> str:
         if valid.bounds:
             return f"const {t} {instr.dest} = ({valid.render()}) ? {lit} : ({t})0;"
         return f"const {t} {instr.dest} = {lit};"
+    if op is Opcode.LOAD and instr.arg[0] in bufs.inline:
+        return inline_load(instr, bufs.inline[instr.arg[0]], bufs)
     if op is Opcode.LOAD:
         buf, index, valid = instr.arg
         ref = load_expr(bufs.dtypes[buf], f"{buf}[{render_index(index, bufs.wide_index)}]")
@@ -192,6 +214,21 @@ def value_line(instr: Instr, bufs: Buffers) -> str:
         ref = load_expr(bufs.dtypes[buf], f"{buf}[{render_index(index, True)}]")
         return f"const {t} {instr.dest} = ({t}){ref};"
     raise NotImplementedError(f"{op} does not define a value")
+
+
+def inline_load(instr: Instr, src: Inlined, bufs: Buffers) -> str:
+    """A load of an inlined producer's output: the producer's body evaluated at the loaded
+    element (its loop variables decoded from the flat index), rounded as its store and this
+    load would round it. Out of a masked load's bounds nothing is evaluated and the value is 0."""
+    t = VALUE_T[instr.value_type]
+    _, index, valid = instr.arg
+    lines = [f"{t} {instr.dest} = ({t})0;"]
+    lines.append(f"if ({valid.render()}) {{" if valid.bounds else "{")
+    lines += decode(list(src.space), f"(i64)({render_index(index, True)})", "  ", True)
+    lines += ["  " + value_line(i, bufs) for i in src.body]
+    lines.append(f"  {instr.dest} = ({t}){load_expr(src.dtype, store_expr(src.dtype, src.result))};")
+    lines.append("}")
+    return "\n".join(lines)
 
 
 @dataclass
@@ -421,8 +458,8 @@ def _vec_width(nest_shape: NestShape, bufs: Buffers, var: str, extent: int) -> i
     return v
 
 
-def signature(name: str, nest: LoopNest, out_dtype: DType, extra: str = "") -> str:
-    params = [f"const {STORE_T[n.dtype]}* __restrict__ in{k}" for k, n in enumerate(nest.kernel.inputs)]
+def signature(name: str, nest: LoopNest, out_dtype: DType, bufs: Buffers, extra: str = "") -> str:
+    params = input_params(nest, bufs)
     params.append(f"{STORE_T[out_dtype]}* __restrict__ out")
     if extra:
         params.append(extra)
@@ -437,7 +474,7 @@ def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned
     inner_var, inner_extent = shape.outer[-1] if shape.outer else ("", 1)
     vec = _vec_width(shape, bufs, inner_var, inner_extent) if shape.outer and write.opcode is Opcode.STORE else 1
     wide = bufs.wide_index or cells > (1 << 30)
-    lines = [signature(nest.name, nest, out_dtype) + " {"]
+    lines = [signature(nest.name, nest, out_dtype, bufs) + " {"]
     groups = cells // vec
     lines.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {groups}LL; g += (i64)gridDim.x * {THREADS}) {{")
     if shape.outer:
@@ -461,7 +498,7 @@ def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned
         lines.append(f"      {buf}[{render_index(index, wide)}] = {store_expr(out_dtype, write.srcs[0])};")
     lines += ["    }", "  }", "}"]
     grid = max(1, min(-(-groups // THREADS), 1 << 20))
-    return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")])
+    return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes={"elementwise": True})
 
 
 SORT_TILE_LIMITS = ((1 << 16, 256), (1 << 20, 1024))  # occurrences -> occurrences per sorted tile
@@ -547,7 +584,7 @@ def plan_scatter(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     tiles = max(1, -(-occurrences // tile))
     block = 64  # one wave: the scan and the tile search below are lane-wide
     col_blocks = max(1, -(-cols // block))
-    params = [f"const {STORE_T[n.dtype]}* __restrict__ in{k}" for k, n in enumerate(nest.kernel.inputs)]
+    params = input_params(nest, bufs)
 
     per = tile // THREADS  # occurrences per thread, held in registers as thread * per + e
     sort = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {nest.name}_sort({", ".join(params + ["unsigned long long* __restrict__ runs"])}) {{']
@@ -729,7 +766,7 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     inner_var, inner_extent = shape.inner[-1]
 
     if group == 1:
-        lines = [signature(nest.name, nest, out_dtype) + " {"]
+        lines = [signature(nest.name, nest, out_dtype, bufs) + " {"]
         lines.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {cells}LL; g += (i64)gridDim.x * {THREADS}) {{")
         lines += decode(shape.outer, "g", "    ", wide)
         lines.append(f"    {acc_t} acc = {ident};")
@@ -761,7 +798,7 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
 
     waves = THREADS // 64
     if group == 64:
-        lines = [signature(nest.name, nest, out_dtype) + " {"]
+        lines = [signature(nest.name, nest, out_dtype, bufs) + " {"]
         lines.append("  const int lane = threadIdx.x & 63;")
         lines.append(f"  for (i64 g = blockIdx.x * (i64){waves} + (threadIdx.x >> 6); g < {cells}LL; g += (i64)gridDim.x * {waves}) {{")
         lines += decode(shape.outer, "g", "    ", wide)
@@ -785,7 +822,7 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
             lines.append("      " + _fold(fold, "acc", f"lds_[{w}]"))
 
     if parts == 1:
-        lines = [signature(nest.name, nest, out_dtype) + " {"]
+        lines = [signature(nest.name, nest, out_dtype, bufs) + " {"]
         lines.append(f"  for (i64 g = blockIdx.x; g < {cells}LL; g += gridDim.x) {{")
         lines += decode(shape.outer, "g", "    ", wide)
         lines.append(f"    {acc_t} acc = {ident};")
@@ -798,7 +835,7 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
 
     # split: partials then an ordered fold per cell
     part_name = nest.name + "_part"
-    params = [f"const {STORE_T[n.dtype]}* __restrict__ in{k}" for k, n in enumerate(nest.kernel.inputs)]
+    params = input_params(nest, bufs)
     params.append(f"{acc_t}* __restrict__ scratch")
     lines = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {part_name}({", ".join(params)}) {{']
     lines.append(f"  const i64 g = blockIdx.x / {parts}, p_ = blockIdx.x % {parts};")
@@ -849,7 +886,7 @@ def plan_columns(nest: LoopNest, shape: NestShape, bufs: Buffers, cells: int, R:
     out_ref = f"out[{render_index(shape.out_index, wide)}]"
     body = ["      " + value_line(i, bufs) for i in shape.body]
     name = nest.name if parts == 1 else nest.name + "_part"
-    params = [f"const {STORE_T[n.dtype]}* __restrict__ in{k}" for k, n in enumerate(nest.kernel.inputs)]
+    params = input_params(nest, bufs)
     params.append(f"{STORE_T[out_dtype]}* __restrict__ out" if parts == 1 else f"{acc_t}* __restrict__ scratch")
     lines = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}({", ".join(params)}) {{']
     lines.append("  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;")
@@ -893,12 +930,16 @@ def plan_columns(nest: LoopNest, shape: NestShape, bufs: Buffers, cells: int, R:
                    notes={"columns": True, "parts": parts})
 
 
-def plan_nest(nest: LoopNest) -> Planned:
+def plan_nest(nest: LoopNest, inlined: "InlineSet | None" = None) -> Planned:
+    """How one nest runs. With `inlined`, loads of the outputs of the producers it names are
+    evaluated in place (see inline_producers)."""
     kernel = nest.kernel
     dtypes = {f"in{k}": n.dtype for k, n in enumerate(kernel.inputs)}
     dtypes["out"] = kernel.target.dtype
     biggest = max([math.prod(n.shape) for n in kernel.inputs] + [math.prod(kernel.target.shape)])
     bufs = Buffers(dtypes, wide_index=biggest >= (1 << 31) - 1)
+    if inlined is not None:
+        inlined.bind(nest, bufs)
     shape = read_nest(nest)
     if shape.fold is None:
         return plan_elementwise(nest, shape, bufs)
@@ -974,22 +1015,160 @@ def epilogue_pairs(nests: list[LoopNest], plans: list[Planned], kept: set | None
     return pairs
 
 
+INLINE_CELLS = 1 << 16  # the largest producer evaluated in its readers instead of launched
+INLINE_BODY = 24  # ... and the most instructions in its body
+
+
+class InlineSet:
+    """Producers evaluated inside their readers, by nest index, and the buffers each reader
+    then needs: every producer it reaches (directly or through another inlined producer) hands
+    its inputs over as `p<j>_in<m>` parameters."""
+
+    def __init__(self, nests: list[LoopNest], producers: set[int]):
+        self.nests = nests
+        self.producers = producers
+        self.by_target = {nests[j].kernel.target: j for j in producers}
+
+    def reached(self, nest: LoopNest) -> list[int]:
+        seen: set[int] = set()
+        stack = [self.by_target[n] for n in nest.kernel.inputs if n in self.by_target]
+        while stack:
+            j = stack.pop()
+            if j in seen:
+                continue
+            seen.add(j)
+            stack += [self.by_target[n] for n in self.nests[j].kernel.inputs if n in self.by_target]
+        return sorted(seen)
+
+    def bind(self, nest: LoopNest, bufs: Buffers) -> None:
+        from dataclasses import replace
+
+        reached = self.reached(nest)
+        if not reached:
+            return
+        names = {j: {f"in{m}": f"p{j}_in{m}" for m in range(len(self.nests[j].kernel.inputs))} for j in reached}
+        for j in reached:
+            for m, node in enumerate(self.nests[j].kernel.inputs):
+                bufs.dtypes[names[j][f"in{m}"]] = node.dtype
+                bufs.extra.append(names[j][f"in{m}"])
+
+        def renamed(instr: Instr, prefix: str, buffers: dict[str, str]) -> Instr:
+            def ix(index: Index) -> Index:
+                return Index(index.const, tuple((prefix + v, c) for v, c in index.terms))
+
+            def vd(valid: Valid) -> Valid:
+                return Valid(tuple((prefix + v, lo, hi, n) for v, lo, hi, n in valid.bounds))
+
+            arg = instr.arg
+            if instr.opcode is Opcode.LOAD:
+                arg = (buffers[arg[0]], ix(arg[1]), vd(arg[2]))
+            elif instr.opcode is Opcode.GATHER:
+                arg = (buffers[arg[0]], ix(arg[1]))
+            elif instr.opcode is Opcode.CONST:
+                arg = (arg[0], vd(arg[1]))
+            return replace(instr, dest=prefix + instr.dest, srcs=tuple(prefix + x for x in instr.srcs), arg=arg)
+
+        sources: dict[int, Inlined] = {}
+        for j in reached:
+            shape = read_nest(self.nests[j])
+            prefix = f"p{j}_"
+            target = self.nests[j].kernel.target
+            space = tuple((prefix + f"i{d}", e) for d, e in enumerate(target.shape))
+            body = tuple(renamed(i, prefix, names[j]) for i in shape.body)
+            sources[j] = Inlined(space, body, prefix + shape.write.srcs[0], target.dtype)
+        for k, node in enumerate(nest.kernel.inputs):
+            if node in self.by_target:
+                bufs.inline[f"in{k}"] = sources[self.by_target[node]]
+        for j in reached:
+            for m, node in enumerate(self.nests[j].kernel.inputs):
+                if node in self.by_target:
+                    bufs.inline[names[j][f"in{m}"]] = sources[self.by_target[node]]
+
+    def extras(self, nest: LoopNest) -> list[tuple[int, int]]:
+        """(producer, input) of each extra parameter, in order."""
+        return [(j, m) for j in self.reached(nest) for m in range(len(self.nests[j].kernel.inputs))]
+
+
+def _stores_its_cells(nest: LoopNest) -> bool:
+    """An elementwise nest that loops over its output shape and stores each cell at its
+    row-major place, so a reader's flat index decodes into its loop variables."""
+    shape = read_nest(nest)
+    if shape.fold is not None or shape.write is None or shape.write.opcode is not Opcode.STORE:
+        return False
+    target = nest.kernel.target.shape
+    if tuple(nest.space) != tuple(target):
+        return False
+    from limn_amd.codegen import contiguous_index
+
+    return shape.write.arg[1] == contiguous_index(tuple(target), [f"i{d}" for d in range(len(target))])
+
+
+def inline_producers(nests: list[LoopNest], plans: list[Planned], kept: set | None, pairs: dict[int, int]) -> set[int]:
+    """Small elementwise nests to evaluate inside their readers instead of launching: the
+    scheduler realizes every broadcast value (a row's max, 1/sum, a LayerNorm scale) as its own
+    kernel (reference limn/schedule.py:46-141), a launch of a few microseconds for a few
+    kilobytes. A producer qualifies when its output is not kept (a sink or a CUSTOM input;
+    `kept` None inlines nothing), it has at most INLINE_CELLS cells and INLINE_BODY
+    instructions, and every reader is an emitted nest (not a contraction, not a relu epilogue)
+    that reads it by plain loads. Its inputs stay valid for the whole plan: the executor keeps
+    every buffer of a transaction and commits assigns only at its end."""
+    if kept is None:
+        return set()
+    fused = set(pairs) | set(pairs.values())
+    readers: dict = {}
+    for c, nest in enumerate(nests):
+        for node in nest.kernel.inputs:
+            readers.setdefault(node, set()).add(c)
+    chosen: set[int] = set()
+    for j, (nest, plan) in enumerate(zip(nests, plans)):
+        target = nest.kernel.target
+        if not plan.notes.get("elementwise") or j in fused or target in kept or target not in readers:
+            continue
+        if math.prod(target.shape) > INLINE_CELLS or len(read_nest(nest).body) > INLINE_BODY:
+            continue
+        if not _stores_its_cells(nest):
+            continue
+        ok = True
+        for c in readers[target]:
+            if c in fused or plans[c].contraction is not None or c <= j:
+                ok = False
+                break
+            name = {f"in{k}" for k, n in enumerate(nests[c].kernel.inputs) if n is target}
+            if any(i.opcode is Opcode.GATHER and i.arg[0] in name for i in nests[c].instrs):
+                ok = False
+                break
+        if ok:
+            chosen.add(j)
+    return chosen
+
+
 def nest_runners(dev, nests: list[LoopNest]):
     """Compile every nest of a plan into one hipRTC program; one runner per nest, in order. A
     contraction whose only reader is a relu nest runs as one MFMA launch with a relu epilogue,
     from the relu nest's runner (see epilogue_pairs)."""
     plans = [plan_nest(n) for n in nests]
-    pairs = epilogue_pairs(nests, plans, getattr(dev, "plan_kept", None))
+    kept = getattr(dev, "plan_kept", None)
+    pairs = epilogue_pairs(nests, plans, kept)
     fused = {j: i for i, j in pairs.items()}
     for j in fused:
         plans[j] = Planned("", [], notes={"epilogue of": nests[fused[j]].name})
+    inlined = InlineSet(nests, inline_producers(nests, plans, kept, pairs))
+    for c, nest in enumerate(nests):
+        if c not in inlined.producers and plans[c].launches and inlined.reached(nest):
+            plans[c] = plan_nest(nest, inlined)
+    for j in inlined.producers:
+        plans[j] = Planned("", [], notes={"inlined": True})
     names = [launch.name for p in plans for launch in p.launches]
     functions = runtime.load_functions(PRELUDE + "\n".join(p.source for p in plans), names) if names else {}
     runners = []
     operands: dict[int, list] = {}  # a fused contraction's inputs, from its call to its relu's
+    producer_inputs: dict[int, list] = {}  # an inlined producer's inputs, from its call to its readers'
     for k, (nest, plan) in enumerate(zip(nests, plans)):
         if k in pairs:
             runners.append(_stash_runner(operands, k))
+            continue
+        if k in inlined.producers:
+            runners.append(_keep_runner(producer_inputs, k))
             continue
         if k in fused:
             runners.append(_epilogue_runner(dev, plans[fused[k]].contraction, operands, fused[k]))
@@ -997,13 +1176,25 @@ def nest_runners(dev, nests: list[LoopNest]):
         if plan.contraction is not None:
             runners.append(_contraction_runner(dev, plan.contraction))
             continue
-        nin = len(nest.kernel.inputs)
+        extras = inlined.extras(nest)
+        nin = len(nest.kernel.inputs) + len(extras)
         launchers = []
         for launch in plan.launches:
             count = {"io": nin + 1, "io_scratch": nin + 1, "io_scratch_out": nin + 2}.get(launch.args, 2)
             launchers.append((launch.args, _launcher(dev, functions[launch.name], launch, count - 1)))
-        runners.append(_make_runner(dev, launchers, plan.scratch_bytes))
+        runners.append(_make_runner(dev, launchers, plan.scratch_bytes, extras, producer_inputs))
     return runners
+
+
+def _keep_runner(producer_inputs: dict, k: int):
+    """An inlined producer's own call: keep its inputs for its readers, launch nothing (its
+    output buffer is never read)."""
+
+    def run(inputs: list, outs: list) -> None:
+        producer_inputs[k] = inputs
+
+    run.launches_nothing = True
+    return run
 
 
 def _matmul_launcher(dev, con: Contraction, epilogue: int):
@@ -1044,6 +1235,7 @@ def _stash_runner(operands: dict, k: int):
     def run(inputs: list, outs: list) -> None:
         operands[k] = inputs
 
+    run.launches_nothing = True
     return run
 
 
@@ -1058,13 +1250,15 @@ def _epilogue_runner(dev, con: Contraction, operands: dict, k: int):
     return run
 
 
-def _make_runner(dev, launchers, scratch_bytes: int):
+def _make_runner(dev, launchers, scratch_bytes: int, extras: list | None = None, producer_inputs: dict | None = None):
     held: list = []
 
     def run(inputs: list, outs: list) -> None:
         if scratch_bytes and not held:
             held.append(dev._alloc(scratch_bytes))
         ins = [b.ptr for b in inputs]
+        if extras:
+            ins += [producer_inputs[j][m].ptr for j, m in extras]
         for kind, launch in launchers:
             if kind == "io":
                 launch(ins + [outs[0].ptr])

@@ -6,6 +6,8 @@ no kernel runs."""
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 
@@ -99,3 +101,73 @@ def test_float32_sum_is_not_a_contraction():
     a = Tensor(rng.standard_normal((64, 64)).astype(np.float32), dtype=float32)
     nests, _ = lowered([(a @ a).relu()])
     assert all(emit.plan_nest(n).contraction is None for n in nests)
+
+
+def inlined_of(sinks: list[Tensor], kept_override=None) -> tuple[list, set[int]]:
+    nests, kept = lowered(sinks)
+    plans = [emit.plan_nest(n) for n in nests]
+    pairs = emit.epilogue_pairs(nests, plans, kept)
+    return nests, emit.inline_producers(nests, plans, kept if kept_override is None else kept_override(kept), pairs)
+
+
+def softmax_layernorm(n: int = 64) -> Tensor:
+    x = Tensor(rng.standard_normal((n, n)).astype(np.float32))
+    y = x.softmax(-1)
+    c = y - y.mean(axis=-1, keepdim=True)
+    return c / ((c * c).mean(axis=-1, keepdim=True) + 1e-5).sqrt()
+
+
+def test_broadcast_producers_of_softmax_layernorm_are_inlined():
+    """The scheduler's 11 kernels (reference limn/schedule.py:46-141): the six per-row and scalar
+    ones (NEG max, 1/sum, 1/n twice, NEG mean, 1/sqrt(var + eps)) run inside their readers."""
+    nests, chosen = inlined_of([softmax_layernorm()])
+    assert len(nests) == 11
+    assert sorted(math.prod(nests[j].kernel.target.shape) for j in chosen) == [1, 1, 64, 64, 64, 64]
+    assert all(emit.plan_nest(nests[j]).notes.get("elementwise") for j in chosen)
+
+
+def test_a_kept_producer_is_not_inlined():
+    x = Tensor(rng.standard_normal((8, 8)).astype(np.float32))
+    neg = -x.max(axis=1, keepdim=True)
+    out = (x + neg).exp()
+    nests, chosen = inlined_of([out, neg])
+    assert not any(nests[j].kernel.target is realized(neg.node) for j in chosen)
+    nests, chosen = inlined_of([out])
+    assert any(nests[j].kernel.target is realized(neg.node) for j in chosen)
+
+
+def test_a_producer_read_by_a_contraction_runs():
+    """The MFMA kernel reads its operands from memory, so a computed operand must be stored."""
+    a, b = operands(64, 64, 64)
+    scaled = a * 2.0
+    nests, chosen = inlined_of([scaled @ b])
+    plans = [emit.plan_nest(n) for n in nests]
+    producer = [j for j, n in enumerate(nests) if n.kernel.target is realized(scaled.node)]
+    assert len(producer) == 1 and any(p.contraction is not None for p in plans)
+    assert chosen == set()
+
+
+def test_a_gathered_table_is_not_inlined():
+    table = Tensor(rng.standard_normal((16, 4)).astype(np.float32)) * 3.0
+    idx = Tensor(rng.integers(0, 16, size=(5,)).astype(np.int32))
+    nests, chosen = inlined_of([table.gather_rows(idx)])
+    assert chosen == set()
+
+
+def test_nothing_is_inlined_without_a_record_of_readers():
+    nests, _ = lowered([softmax_layernorm()])
+    plans = [emit.plan_nest(n) for n in nests]
+    assert emit.inline_producers(nests, plans, None, {}) == set()
+
+
+def test_a_reader_of_an_inlined_producer_takes_its_inputs_as_parameters():
+    nests, chosen = inlined_of([softmax_layernorm()])
+    inl = emit.InlineSet(nests, chosen)
+    last = nests[-1]
+    plan = emit.plan_nest(last, inl)
+    header = plan.source.split("{", 1)[0]
+    for j, m in inl.extras(last):
+        assert f"p{j}_in{m}" in header
+    # every load of an inlined producer's output became an evaluation of its body
+    inlined_inputs = {f"in{k}" for k, n in enumerate(last.kernel.inputs) if n in inl.by_target}
+    assert inlined_inputs and not any(f"{name}[" in plan.source for name in inlined_inputs)

@@ -139,6 +139,38 @@ def test_scatter_grid_covers_more_rows_than_one_launch(hipdev):
     check(hipdev, scatter_rows(values, idx, (rows, 1)), bitwise=True)
 
 
+def launch_free_calls(hipdev, sinks) -> int:
+    """How many of the plan's calls launch nothing (their nest runs inside its readers)."""
+    hipdev.record = []
+    hipdev.execute(sinks)
+    plan = hipdev.record[0].plan
+    hipdev.record = None
+    return sum(1 for call in plan.calls if getattr(call.fn, "launches_nothing", False))
+
+
+def test_softmax_layernorm_with_inlined_row_statistics(hipdev):
+    """The six per-row and scalar kernels of softmax -> LayerNorm run inside their readers; the
+    result still matches the oracle."""
+    x = Tensor(randf(300, 257))
+    y = x.softmax(-1)
+    c = y - y.mean(axis=-1, keepdim=True)
+    out = c / ((c * c).mean(axis=-1, keepdim=True) + 1e-5).sqrt()
+    assert launch_free_calls(hipdev, [out.node]) == 6
+    check(hipdev, out, rtol=1e-4, atol=1e-5)
+
+
+def test_inlined_producer_read_through_a_pad_and_a_gather_index(hipdev):
+    """An inlined producer read through a masked view (zero outside, nothing evaluated there)
+    and one that computes gather indices."""
+    x = Tensor(randf(8, 5))
+    s = x.max(axis=1, keepdim=True) * 2.0
+    padded = s.pad(((1, 1), (0, 0))) * Tensor(randf(10, 16))
+    check(hipdev, padded, exact=True)
+    idx = Tensor(rng.integers(0, 7, size=(6,)).astype(np.int32))
+    shifted = Tensor(randf(9, 3)).gather_rows(idx + Tensor(np.ones(6, np.int32)))
+    check(hipdev, shifted * 1.5, exact=True)
+
+
 def test_scatter_int32_is_exact(hipdev):
     from limn_amd.tensor import scatter_rows
 
