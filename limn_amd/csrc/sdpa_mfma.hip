@@ -915,6 +915,265 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_dma(const u16* __restr
   store_transposed<T, D>(dv + b * (int64_t)t_k * D, gv, key, t_k, 1.f);
 }
 
+// ---- forward at D = 128: streamed K and V tiles copied straight into LDS ------------------------
+// The same swizzled tiles and LDS DMA as the dK/dV pass above: K is read as row operands of
+// S^T = K Q^T, V through the transposing reads of O^T += V^T P^T. Tiles that need masking (a
+// causal block's two diagonal tiles, a last tile past t_k, every tile under a key mask) run
+// their own instance of the tile body.
+
+// one 64-key tile against the wave's 32 resident queries: per 32-key half, S^T, the online
+// softmax step (the reference point moves only when a half's max passes it by `lift`), then the
+// V^T P^T products
+template <typename T, bool CAUSAL, bool MASK, bool EDGE>
+__device__ __forceinline__ void fwd_tile128(const u16* Kb, const u16* Vb, const SwzReads128& ad, int k0, int row, int t_k,
+                                            float c2, float lift, uint64_t live, const u16x8 (&qf)[8], f32x16 (&acc)[4],
+                                            float& m, float& l) {
+  const int lane = threadIdx.x & 63, h = lane >> 5;
+#pragma unroll
+  for (int sub = 0; sub < 2; sub++) {
+    f32x16 s = zero16();
+#pragma unroll
+    for (int ds = 0; ds < 8; ds++) s = T::mfma32(ad.rows(Kb, sub, ds), qf[ds], s);
+    if (EDGE) {
+      const unsigned mb = (unsigned)(live >> (sub * 32 + 4 * h));
+#pragma unroll
+      for (int i = 0; i < 16; i++) s[i] = hidden<CAUSAL, MASK>(k0, sub, i, h, t_k, row, mb) ? neg_inf() : s[i];
+    }
+    float mx = neg_inf();
+#pragma unroll
+    for (int i = 0; i < 16; i++) mx = fmaxf(mx, s[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    if (__any(mx > m + lift)) {
+      const float mnew = fmaxf(m, mx);
+      const float alpha = mnew == neg_inf() ? 1.f : fast_exp2((m - mnew) * c2);
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; dt++) acc[dt] *= alpha;
+      m = mnew;
+    }
+    const float base = m == neg_inf() ? 0.f : m * c2;
+    float rs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float p = fast_exp2(fmaf(s[i], c2, -base));
+      s[i] = p;
+      rs += p;
+    }
+    l += rs;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const u16x8 pb = pack8<T>(s, 8 * c);
+#pragma unroll
+      for (int dt = 0; dt < 4; dt++) acc[dt] = T::mfma32(ad.transposed(Vb, sub * 32 + 16 * c, dt), pb, acc[dt]);
+    }
+  }
+}
+
+template <typename T, bool CAUSAL, bool MASK>
+__global__ __launch_bounds__(THREADS, 2) void sdpa_fwd_dma(const u16* __restrict__ q, const u16* __restrict__ k,
+                                                           const u16* __restrict__ v, const u16* __restrict__ mask,
+                                                           u16* __restrict__ out, float* __restrict__ lse, int64_t batch,
+                                                           int t_q, int t_k, float scale) {
+  constexpr int D = 128, ROWS = 128;
+  __shared__ __attribute__((aligned(1024))) u16 K0[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 K1[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 V0[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 V1[TILE * D];
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
+  const int64_t nqb = (t_q + ROWS - 1) / ROWS;
+  int64_t b, blk;
+  head_and_block(batch, nqb, b, blk);
+  const int64_t qb = nqb - 1 - blk;  // causal: the longest rows go first
+  const int q0 = (int)qb * ROWS, row = q0 + wave * 32 + n;
+  const Rows qrows(q + b * (int64_t)t_q * D, t_q, D);
+  const DmaTile128 kd(k + b * (int64_t)t_k * D, t_k, wave, lane), vd(v + b * (int64_t)t_k * D, t_k, wave, lane);
+  const SwzReads128 ad(lane);
+  const MaskRow mrow(MASK ? mask + b * (int64_t)t_k : nullptr, t_k);
+  const float c2 = scale * LOG2E, lift = RESCALE_LOG2 / c2;  // scale > 0 (the C ABI routes others away)
+
+  u16x8 qf[8];
+  f32x16 acc[4];
+  float m = neg_inf(), l = 0.f;
+#pragma unroll
+  for (int ds = 0; ds < 8; ds++) qf[ds] = qrows.load8(row * D + ds * 16 + 8 * h);
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++) acc[dt] = zero16();
+
+  const int kend = CAUSAL ? (q0 + ROWS < t_k ? q0 + ROWS : t_k) : t_k;
+  const int ntiles = (kend + TILE - 1) / TILE;
+  // tile it from (Kc, Vc) while tile it + 1 is copied into the idle buffers (every wave left them
+  // at the last barrier), then the wait for the copy and the barrier
+  auto step = [&](auto edge, int it, const u16* Kc, const u16* Vc, u16* Kn, u16* Vn) __attribute__((always_inline)) {
+    const int k0 = it * TILE;
+    kd.copy(Kn, k0 + TILE, wave);
+    vd.copy(Vn, k0 + TILE, wave);
+    const uint64_t live = MASK ? live_keys<T>(mrow.load(k0 + lane)) : ~0ull;
+    fwd_tile128<T, CAUSAL, MASK, decltype(edge)::value>(Kc, Vc, ad, k0, row, t_k, c2, lift, live, qf, acc, m, l);
+    __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
+    __syncthreads();
+  };
+  // tiles [from, to) with one body: tile it is in buffer it % 2
+  auto run = [&](auto edge, int from, int to) __attribute__((always_inline)) {
+    int it = from;
+    if ((it & 1) && it < to) {
+      step(edge, it, K1, V1, K0, V0);
+      it++;
+    }
+    for (; it + 1 < to; it += 2) {
+      step(edge, it, K0, V0, K1, V1);
+      step(edge, it + 1, K1, V1, K0, V0);
+    }
+    if (it < to) step(edge, it, K0, V0, K1, V1);
+  };
+  if (ntiles > 0) {
+    kd.copy(K0, 0, wave);
+    vd.copy(V0, 0, wave);
+    __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
+    __syncthreads();
+  }
+  // unmasked: every key of the tile exists and, under causality, precedes the block's first row
+  int open = MASK ? 0 : t_k / TILE;
+  if (CAUSAL && q0 / TILE < open) open = q0 / TILE;
+  if (open > ntiles) open = ntiles;
+  run(std::false_type{}, 0, open);
+  run(std::true_type{}, open, ntiles);
+  const float total = l + __shfl_xor(l, 32);
+  store_transposed<T, D>(out + b * (int64_t)t_q * D, acc, row, t_q, 1.f / total);
+  if (h == 0 && row < t_q) lse[b * (int64_t)t_q + row] = m * scale + logf(total);
+}
+
+// ---- dQ pass at D = 128: streamed K and V tiles copied straight into LDS ------------------------
+// K serves as the row operand of S = Q K^T (taken as S^T = K Q^T) and through transposing reads
+// as the operand of dQ^T += K^T dS^T; V as the row operand of dP^T = V dO^T.
+
+// one 64-key tile against the wave's 32 resident queries: per 32-key half, S^T and dP^T, the
+// probabilities from the saved log-sum-exp, dS, then the K^T dS^T products
+template <typename T, bool CAUSAL, bool MASK, bool EDGE>
+__device__ __forceinline__ void q_tile128(const u16* Kb, const u16* Vb, const SwzReads128& ad, int k0, int row, int t_k,
+                                          float c2, float scale, float L2, float Dr, uint64_t live,
+                                          const u16x8 (&qf)[8], const u16x8 (&of)[8], f32x16 (&acc)[4]) {
+  const int lane = threadIdx.x & 63, h = lane >> 5;
+#pragma unroll
+  for (int sub = 0; sub < 2; sub++) {
+    f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+    for (int ds = 0; ds < 8; ds++) {
+      s = T::mfma32(ad.rows(Kb, sub, ds), qf[ds], s);
+      dp = T::mfma32(ad.rows(Vb, sub, ds), of[ds], dp);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) s[i] = fast_exp2(fmaf(s[i], c2, -L2));
+    if (EDGE) {
+      const unsigned mb = (unsigned)(live >> (sub * 32 + 4 * h));
+#pragma unroll
+      for (int i = 0; i < 16; i++) s[i] = hidden<CAUSAL, MASK>(k0, sub, i, h, t_k, row, mb) ? 0.f : s[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) s[i] *= fmaf(dp[i], scale, -Dr);
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const u16x8 g = pack8<T>(s, 8 * c);
+#pragma unroll
+      for (int dt = 0; dt < 4; dt++) acc[dt] = T::mfma32(ad.transposed(Kb, sub * 32 + 16 * c, dt), g, acc[dt]);
+    }
+  }
+  // per half: the S/dP MFMAs with their 16 row reads (4 ahead), the probabilities and dS, then the
+  // dQ MFMAs with their 16 transposing reads (4 ahead)
+#pragma unroll
+  for (int sub = 0; sub < 2; sub++) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int q = 0; q < 12; q++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 200, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int q = 0; q < 6; q++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  }
+}
+
+template <typename T, bool CAUSAL, bool MASK>
+__global__ __launch_bounds__(THREADS, 2) void sdpa_bwd_q_dma(const u16* __restrict__ q, const u16* __restrict__ k,
+                                                             const u16* __restrict__ v, const u16* __restrict__ dout,
+                                                             const float* __restrict__ lse,
+                                                             const float* __restrict__ delta,
+                                                             const u16* __restrict__ mask, u16* __restrict__ dq,
+                                                             int64_t batch, int t_q, int t_k, float scale) {
+  constexpr int D = 128, ROWS = 128;
+  __shared__ __attribute__((aligned(1024))) u16 K0[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 K1[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 V0[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 V1[TILE * D];
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
+  const int64_t nqb = (t_q + ROWS - 1) / ROWS;
+  int64_t b, blk;
+  head_and_block(batch, nqb, b, blk);
+  const int64_t qb = nqb - 1 - blk;  // causal: the longest rows go first
+  const int q0 = (int)qb * ROWS, row = q0 + wave * 32 + n;
+  const Rows qrows(q + b * (int64_t)t_q * D, t_q, D), orows(dout + b * (int64_t)t_q * D, t_q, D);
+  const DmaTile128 kd(k + b * (int64_t)t_k * D, t_k, wave, lane), vd(v + b * (int64_t)t_k * D, t_k, wave, lane);
+  const SwzReads128 ad(lane);
+  const MaskRow mrow(MASK ? mask + b * (int64_t)t_k : nullptr, t_k);
+  const float c2 = scale * LOG2E;
+
+  u16x8 qf[8], of[8];
+  f32x16 acc[4];
+#pragma unroll
+  for (int ds = 0; ds < 8; ds++) {
+    qf[ds] = qrows.load8(row * D + ds * 16 + 8 * h);
+    of[ds] = orows.load8(row * D + ds * 16 + 8 * h);
+  }
+  const float L2 = row < t_q ? lse[b * (int64_t)t_q + row] * LOG2E : 0.f;
+  const float Dr = row < t_q ? delta[b * (int64_t)t_q + row] * scale : 0.f;  // ds = p (dp scale - delta scale)
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++) acc[dt] = zero16();
+
+  const int kend = CAUSAL ? (q0 + ROWS < t_k ? q0 + ROWS : t_k) : t_k;
+  const int ntiles = (kend + TILE - 1) / TILE;
+  auto step = [&](auto edge, int it, const u16* Kc, const u16* Vc, u16* Kn, u16* Vn) __attribute__((always_inline)) {
+    const int k0 = it * TILE;
+    kd.copy(Kn, k0 + TILE, wave);
+    vd.copy(Vn, k0 + TILE, wave);
+    const uint64_t live = MASK ? live_keys<T>(mrow.load(k0 + lane)) : ~0ull;
+    q_tile128<T, CAUSAL, MASK, decltype(edge)::value>(Kc, Vc, ad, k0, row, t_k, c2, scale, L2, Dr, live, qf, of, acc);
+    __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
+    __syncthreads();
+  };
+  auto run = [&](auto edge, int from, int to) __attribute__((always_inline)) {
+    int it = from;
+    if ((it & 1) && it < to) {
+      step(edge, it, K1, V1, K0, V0);
+      it++;
+    }
+    for (; it + 1 < to; it += 2) {
+      step(edge, it, K0, V0, K1, V1);
+      step(edge, it + 1, K1, V1, K0, V0);
+    }
+    if (it < to) step(edge, it, K0, V0, K1, V1);
+  };
+  if (ntiles > 0) {
+    kd.copy(K0, 0, wave);
+    vd.copy(V0, 0, wave);
+    __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
+    __syncthreads();
+  }
+  int open = MASK ? 0 : t_k / TILE;
+  if (CAUSAL && q0 / TILE < open) open = q0 / TILE;
+  if (open > ntiles) open = ntiles;
+  run(std::false_type{}, 0, open);
+  run(std::true_type{}, open, ntiles);
+  store_transposed<T, D>(dq + b * (int64_t)t_q * D, acc, row, t_q, 1.f);
+}
+
 // ---------------------------------------------------------------------------------------------
 
 // Resident 32-row tiles per wave for each pass and head dim: 2 (each LDS operand read feeds two
@@ -938,10 +1197,17 @@ int launch_nt(const SdpaArgs& a) {
   const dim3 grid((unsigned)blocks), block(THREADS);
   const float scale = (float)a.scale;
   const u16* mask = (const u16*)a.mask;
-  if constexpr (PASS == SDPA_FWD) {
+  if constexpr (PASS == SDPA_FWD && D == 128) {
+    hipLaunchKernelGGL((sdpa_fwd_dma<T, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q, (const u16*)a.k,
+                       (const u16*)a.v, mask, (u16*)a.out0, (float*)a.out1, a.batch, (int)a.t_q, (int)a.t_k, scale);
+  } else if constexpr (PASS == SDPA_FWD) {
     hipLaunchKernelGGL((sdpa_fwd_mfma<T, D, NT, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q,
                        (const u16*)a.k, (const u16*)a.v, mask, (u16*)a.out0, (float*)a.out1, a.batch, (int)a.t_q, (int)a.t_k,
                        scale);
+  } else if constexpr (PASS == SDPA_BWD_Q && D == 128) {
+    hipLaunchKernelGGL((sdpa_bwd_q_dma<T, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q, (const u16*)a.k,
+                       (const u16*)a.v, (const u16*)a.dout, (const float*)a.lse, (const float*)a.delta, mask,
+                       (u16*)a.out0, a.batch, (int)a.t_q, (int)a.t_k, scale);
   } else if constexpr (PASS == SDPA_BWD_Q) {
     hipLaunchKernelGGL((sdpa_bwd_q_mfma<T, D, NT, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q,
                        (const u16*)a.k, (const u16*)a.v, (const u16*)a.dout, (const float*)a.lse, (const float*)a.delta,
