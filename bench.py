@@ -652,8 +652,8 @@ def main() -> int:
     names = ["sdpa", "sdpa_bwd_q", "sdpa_bwd_kv"]
     # the template instance each CUSTOM name runs at this configuration (rocprofv3's kernel names)
     KERNEL_SYMBOL = {
-        "sdpa": "sdpa_fwd_mfma<BF16,128,1,true,false>",
-        "sdpa_bwd_q": "sdpa_bwd_q_mfma<BF16,128,1,true,false>",
+        "sdpa": "sdpa_fwd_dma<BF16,true,false>",
+        "sdpa_bwd_q": "sdpa_bwd_q_dma<BF16,true,false>",
         "sdpa_bwd_kv": "sdpa_bwd_kv_dma<BF16,true,false>",
     }
     dom = int(np.argmax(per))

@@ -477,15 +477,40 @@ def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned
     lines = [signature(nest.name, nest, out_dtype, bufs) + " {"]
     groups = cells // vec
     lines.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {groups}LL; g += (i64)gridDim.x * {THREADS}) {{")
+    # A masked load whose mask does not involve the stride-1 var is valid for the whole VEC run
+    # or for none of it: its pointer is chosen once per run (the buffer's start when masked, which
+    # is in bounds for VEC elements) and the run's loads are unconditional, so they merge into one
+    # vector load instead of VEC branches around 2-byte loads.
+    runs: dict[str, list[str]] = {}
+    pre: list[str] = []
+    if shape.outer and vec > 1 and write.opcode is Opcode.STORE:
+        sizes = {f"in{k}": math.prod(n.shape) for k, n in enumerate(nest.kernel.inputs)}
+        for instr in shape.body:
+            if instr.opcode is not Opcode.LOAD:
+                continue
+            buf, index, valid = instr.arg
+            if buf in bufs.inline or not valid.bounds or any(b[0] == inner_var for b in valid.bounds):
+                continue
+            if dict(index.terms).get(inner_var) != 1 or sizes.get(buf, 0) < vec:
+                continue
+            d, t, dt = instr.dest, VALUE_T[instr.value_type], bufs.dtypes[buf]
+            first = Index(index.const, tuple((f"({inner_var}_b * {vec})" if v == inner_var else v, c) for v, c in index.terms))
+            pre.append(f"    const bool {d}_ok = {valid.render()};")
+            pre.append(f"    const {STORE_T[dt]}* {d}_p = {buf} + ({d}_ok ? (i64)({render_index(first, True)}) : (i64)0);")
+            runs[d] = [f"const {t} {d}_raw = ({t}){load_expr(dt, f'{d}_p[j_]')};", f"const {t} {d} = {d}_ok ? {d}_raw : ({t})0;"]
     if shape.outer:
         base_vars = shape.outer[:-1] + [(inner_var + "_b", inner_extent // vec)]
         lines += decode(base_vars, "g", "    ", wide)
+        lines += pre
         lines.append("#pragma unroll")
         lines.append(f"    for (int j_ = 0; j_ < {vec}; j_++) {{")
         lines.append(f"      const int {inner_var} = {inner_var}_b * {vec} + j_;")
     else:
         lines.append("    {")
     for instr in shape.body:
+        if instr.dest in runs:
+            lines += ["      " + ln for ln in runs[instr.dest]]
+            continue
         lines.append("      " + value_line(instr, bufs))
     buf, index = write.arg
     if write.opcode is Opcode.SCATTER:
@@ -797,6 +822,34 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
         return out
 
     waves = THREADS // 64
+    if group == 64 and chunks < 64:
+        # a short row: G lanes (the power of two covering its VEC-wide chunks) per cell, 64 / G
+        # cells per wave, so a wave's loads cover whole consecutive rows; a butterfly within each
+        # group of lanes folds the cell
+        G = 1
+        while G < chunks:
+            G *= 2
+        per_wave = 64 // G
+        lines = [signature(nest.name, nest, out_dtype, bufs) + " {"]
+        lines.append(f"  const int lane = threadIdx.x & 63, sub_ = lane % {G};")
+        lines.append(f"  for (i64 g0 = (blockIdx.x * (i64){waves} + (threadIdx.x >> 6)) * {per_wave}; g0 < {cells}LL; g0 += (i64)gridDim.x * {waves * per_wave}) {{")
+        lines.append(f"    const i64 g = g0 + lane / {G};")
+        lines.append(f"    {acc_t} acc = {ident};")
+        lines.append(f"    if (g < {cells}LL) {{")
+        lines += ["  " + ln for ln in decode(shape.outer, "g", "    ", wide)]
+        lines += ["  " + ln for ln in strided_loop("sub_", f"{chunks}LL", G)]
+        lines.append("    }")
+        k = G // 2
+        while k > 0:
+            op = "fadd" if fold is Op.ADD else "fmax_nan"
+            lines.append(f"    acc = {op}(acc, ({acc_t})__shfl_xor(acc, {k}));")
+            k //= 2
+        lines.append(f"    if (sub_ == 0 && g < {cells}LL) {{")
+        lines += ["  " + ln for ln in decode(shape.outer, "g", "    ", wide)]
+        lines.append(f"      {out_ref} = {store_expr(out_dtype, 'acc')};")
+        lines += ["    }", "  }", "}"]
+        grid = max(1, min(-(-cells // (waves * per_wave)), 1 << 20))
+        return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes={"group": G, "vec": vec})
     if group == 64:
         lines = [signature(nest.name, nest, out_dtype, bufs) + " {"]
         lines.append("  const int lane = threadIdx.x & 63;")
@@ -846,19 +899,44 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     block_fold(lines)
     lines.append("      scratch[blockIdx.x] = acc;")
     lines += ["    }", "}"]
-    final = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {nest.name}(const {acc_t}* __restrict__ scratch, {STORE_T[out_dtype]}* __restrict__ out) {{']
-    final.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {cells}LL; g += (i64)gridDim.x * {THREADS}) {{")
-    final += decode(shape.outer, "g", "    ", wide)
-    final.append(f"    {acc_t} acc = scratch[g * {parts}];")
-    final.append(f"    for (int p_ = 1; p_ < {parts}; p_++) " + _fold(fold, "acc", f"scratch[g * {parts} + p_]"))
-    final.append(f"    {out_ref} = {store_expr(out_dtype, 'acc')};")
-    final += ["  }", "}"]
+    final, final_grid = fold_parts(nest.name, shape, acc_t, out_dtype, out_ref, wide, cells, parts, ident, "g * {parts} + p_".format(parts=parts))
     source = "\n".join(lines) + "\n" + "\n".join(final)
     launches = [
         Launch(part_name, cells * parts, THREADS, "io_scratch"),
-        Launch(nest.name, max(1, min(-(-cells // THREADS), 1 << 20)), THREADS, "scratch_out"),
+        Launch(nest.name, final_grid, THREADS, "scratch_out"),
     ]
     return Planned(source, launches, scratch_bytes=cells * parts * acc_dt.itemsize, notes={"parts": parts, "vec": vec})
+
+
+def fold_parts(name: str, shape: NestShape, acc_t: str, out_dtype: DType, out_ref: str, wide: bool, cells: int, parts: int,
+               ident: str, at: str) -> tuple[list[str], int]:
+    """The kernel that folds each cell's partial totals (`scratch[at]`, `at` in g and p_) and
+    stores the cell. A thread per cell folds them in part order; past 16 parts a wave takes a
+    cell, its lanes folding parts lane, lane + 64, ... and a fixed butterfly folding the lanes,
+    so a cell's chain of dependent loads is parts / 64 long instead of parts."""
+    fold = shape.fold
+    lines = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}(const {acc_t}* __restrict__ scratch, {STORE_T[out_dtype]}* __restrict__ out) {{']
+    if parts <= 16:
+        lines.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {cells}LL; g += (i64)gridDim.x * {THREADS}) {{")
+        lines += decode(shape.outer, "g", "    ", wide)
+        lines.append("    int p_ = 0;")
+        lines.append(f"    {acc_t} acc = scratch[{at}];")
+        lines.append(f"    for (p_ = 1; p_ < {parts}; p_++) " + _fold(fold, "acc", f"scratch[{at}]"))
+        lines.append(f"    {out_ref} = {store_expr(out_dtype, 'acc')};")
+        lines += ["  }", "}"]
+        return lines, max(1, min(-(-cells // THREADS), 1 << 20))
+    waves = THREADS // 64
+    wave_fold = "wave_fold_add" if fold is Op.ADD else "wave_fold_max"
+    lines.append("  const int lane = threadIdx.x & 63;")
+    lines.append(f"  for (i64 g = blockIdx.x * (i64){waves} + (threadIdx.x >> 6); g < {cells}LL; g += (i64)gridDim.x * {waves}) {{")
+    lines.append(f"    {acc_t} acc = {ident};")
+    lines.append(f"    for (int p_ = lane; p_ < {parts}; p_ += 64) " + _fold(fold, "acc", f"scratch[{at}]"))
+    lines.append(f"    acc = {wave_fold}(acc);")
+    lines.append("    if (lane == 0) {")
+    lines += decode(shape.outer, "g", "      ", wide)
+    lines.append(f"      {out_ref} = {store_expr(out_dtype, 'acc')};")
+    lines += ["    }", "  }", "}"]
+    return lines, max(1, min(-(-cells // waves), 1 << 20))
 
 
 COLUMN_TILE = 64  # cells per workgroup of a column reduce: one wave's lanes, one coalesced row piece
@@ -918,14 +996,8 @@ def plan_columns(nest: LoopNest, shape: NestShape, bufs: Buffers, cells: int, R:
     launches = [Launch(name, tiles * parts, THREADS, "io" if parts == 1 else "io_scratch")]
     if parts == 1:
         return Planned("\n".join(lines), launches, notes={"columns": True, "parts": 1})
-    final = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {nest.name}(const {acc_t}* __restrict__ scratch, {STORE_T[out_dtype]}* __restrict__ out) {{']
-    final.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {cells}LL; g += (i64)gridDim.x * {THREADS}) {{")
-    final += decode(shape.outer, "g", "    ", wide)
-    final.append(f"    {acc_t} acc = scratch[g];")
-    final.append(f"    for (int p_ = 1; p_ < {parts}; p_++) " + _fold(fold, "acc", f"scratch[p_ * {cells}LL + g]"))
-    final.append(f"    {out_ref} = {store_expr(out_dtype, 'acc')};")
-    final += ["  }", "}"]
-    launches.append(Launch(nest.name, max(1, min(-(-cells // THREADS), 1 << 20)), THREADS, "scratch_out"))
+    final, final_grid = fold_parts(nest.name, shape, acc_t, out_dtype, out_ref, wide, cells, parts, ident, f"p_ * {cells}LL + g")
+    launches.append(Launch(nest.name, final_grid, THREADS, "scratch_out"))
     return Planned("\n".join(lines) + "\n" + "\n".join(final), launches, scratch_bytes=cells * parts * acc_dt.itemsize,
                    notes={"columns": True, "parts": parts})
 

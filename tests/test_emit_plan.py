@@ -171,3 +171,24 @@ def test_a_reader_of_an_inlined_producer_takes_its_inputs_as_parameters():
     # every load of an inlined producer's output became an evaluation of its body
     inlined_inputs = {f"in{k}" for k, n in enumerate(last.kernel.inputs) if n in inl.by_target}
     assert inlined_inputs and not any(f"{name}[" in plan.source for name in inlined_inputs)
+
+
+def test_short_rows_take_a_group_of_lanes_per_cell():
+    """A 64-element bf16 row is 8 runs of 8: 8 lanes fold it, 8 rows per wave."""
+    a = Tensor(rng.standard_normal((8, 300, 64)).astype(np.float32), dtype=bfloat16)
+    nests, _ = lowered([a.cast(float32).sum(axis=-1)])
+    plan = emit.plan_nest(nests[-1])
+    assert plan.notes["group"] == 8 and plan.notes["vec"] == 8
+    assert "__shfl_xor(acc, 4)" in plan.source and "__shfl_xor(acc, 8)" not in plan.source
+
+
+def test_a_load_masked_by_an_outer_dim_reads_whole_runs():
+    parts = [Tensor(rng.standard_normal((1, 6, 40)).astype(np.float32), dtype=bfloat16) for _ in range(3)]
+    stacked = parts[0].pad(((0, 2), (0, 0), (0, 0))) + parts[1].pad(((1, 1), (0, 0), (0, 0))) + parts[2].pad(((2, 0), (0, 0), (0, 0)))
+    nests, _ = lowered([stacked])
+    source = emit.plan_nest(nests[-1]).source
+    assert source.count("_ok ?") == 6 and source.count("_p[j_]") == 3
+    # a pad along the stride-1 dim keeps the per-element form
+    inner = Tensor(rng.standard_normal((6, 40)).astype(np.float32)).pad(((0, 0), (4, 4)))
+    nests, _ = lowered([inner * 2.0])
+    assert "_p[j_]" not in emit.plan_nest(nests[-1]).source

@@ -44,13 +44,30 @@ def test_corpus_at_size(hipdev, name):
 
 @pytest.mark.parametrize(
     "shape,axis",
-    [((3, 10), 1), ((9000, 70), 1), ((700, 3000), 1), ((64, 9000), 1), ((4, 300000), 1), ((3000, 40), 0), ((40, 3000), 0), ((2, 3, 4000, 5), (1, 2))],
-    ids=["tiny", "thread-per-cell", "wave-per-cell", "workgroup-per-cell", "split", "accum-columns", "accum-few-columns", "two-axes"],
+    [((3, 10), 1), ((9000, 70), 1), ((700, 3000), 1), ((64, 9000), 1), ((4, 300000), 1), ((3000, 40), 0), ((40, 3000), 0), ((2, 3, 4000, 5), (1, 2)), ((5000, 64), 1), ((777, 72), 1)],
+    ids=["tiny", "thread-per-cell", "wave-per-cell", "workgroup-per-cell", "split", "accum-columns", "accum-few-columns", "two-axes", "lanes-per-cell", "ragged-lanes-per-cell"],
 )
 def test_every_reduce_form(hipdev, shape, axis):
     x = Tensor(rng.standard_normal(shape).astype(np.float32))
     check(hipdev, x.sum(axis=axis), rtol=1e-4, atol=1e-3)
     check(hipdev, x.max(axis=axis), exact=True)
+
+
+def test_short_bf16_rows_reduce_in_lane_groups(hipdev):
+    """Rows of 64 bf16 (the attention delta's shape): 8 lanes per row, 8 rows per wave."""
+    a = Tensor(randf(2, 4, 300, 64), dtype=bfloat16)
+    b = Tensor(randf(2, 4, 300, 64), dtype=bfloat16)
+    check(hipdev, (a.cast(float32) * b.cast(float32)).sum(axis=-1, keepdim=True), rtol=1e-4, atol=1e-4)
+    check(hipdev, a.max(axis=-1), exact=True)
+
+
+@pytest.mark.parametrize("dtype", [float32, bfloat16], ids=str)
+def test_concatenation_by_pads_loads_whole_runs(hipdev, dtype):
+    """Three tensors stacked along a new leading dim by pad-and-add (how a gradient of a split
+    is formed): each load is masked by the leading dim only."""
+    parts = [Tensor(randf(1, 6, 40), dtype=dtype) for _ in range(3)]
+    stacked = parts[0].pad(((0, 2), (0, 0), (0, 0))) + parts[1].pad(((1, 1), (0, 0), (0, 0))) + parts[2].pad(((2, 0), (0, 0), (0, 0)))
+    check(hipdev, stacked, exact=True)
 
 
 def test_max_propagates_nan(hipdev):
@@ -79,25 +96,31 @@ def test_gather_rows(hipdev):
     check(hipdev, table[idx], exact=True)
 
 
-def order_sensitive(*shape: int) -> np.ndarray:
-    """Values whose float sum depends on the order of the adds: large terms that cancel among
-    small ones, so a reordering moves the small ones' rounding."""
-    big = rng.choice(np.array([3e7, -3e7, 1e8, -1e8], np.float32), size=shape)
-    small = rng.uniform(-4, 4, shape).astype(np.float32)
-    return np.where(rng.random(shape) < 0.3, big, small).astype(np.float32)
+def order_sensitive(*shape: int, seed: int = 0) -> np.ndarray:
+    """Values whose float sum tends to depend on the order of the adds: large terms that cancel
+    among small ones, so a reordering moves the small ones' rounding."""
+    r = np.random.default_rng(seed)
+    big = r.choice(np.array([3e7, -3e7, 1e8, -1e8], np.float32), size=shape)
+    small = r.uniform(-4, 4, shape).astype(np.float32)
+    return np.where(r.random(shape) < 0.3, big, small).astype(np.float32)
 
 
 def test_scatter_with_repeats(hipdev):
     """512 values land on one row (reference tests/test_backend_cuda.py:125-131 allows 1e-4 for
-    its atomics); here the total is np.add.at's, bit for bit."""
+    its atomics); here the total is np.add.at's, bit for bit. The values are drawn until adding
+    them in reverse gives other bits, so that an unordered sum would fail."""
     from limn_amd.tensor import scatter_rows
 
-    values = order_sensitive(512, 8)
     idx = np.zeros(512, dtype=np.int32)
-    forward, backward = np.zeros((4, 8), np.float32), np.zeros((4, 8), np.float32)
-    np.add.at(forward, idx, values)
-    np.add.at(backward, idx[::-1], values[::-1])
-    assert np.any(forward != backward), "the values must be order-sensitive for this test to mean anything"
+    for seed in range(100):
+        values = order_sensitive(512, 8, seed=seed)
+        forward, backward = np.zeros((4, 8), np.float32), np.zeros((4, 8), np.float32)
+        np.add.at(forward, idx, values)
+        np.add.at(backward, idx[::-1], values[::-1])
+        if np.any(forward != backward):
+            break
+    else:
+        raise AssertionError("no order-sensitive draw in 100 seeds")
     check(hipdev, scatter_rows(Tensor(values), Tensor(idx), (4, 8)), bitwise=True)
 
 
