@@ -50,6 +50,9 @@ INTS = (int32, int16, int8)
 
 PRELUDE = r"""
 typedef long long i64;
+// every pointer a kernel takes is the start of a device allocation (views are index arithmetic),
+// so 16-byte runs along the stride-1 dim may be one vector access
+#define ALIGNED __attribute__((align_value(16)))
 __device__ __forceinline__ float b2f(unsigned short b) { return __uint_as_float(((unsigned)b) << 16); }
 __device__ __forceinline__ unsigned short f2b(float x) { __bf16 h = (__bf16)x; return __builtin_bit_cast(unsigned short, h); }
 __device__ __forceinline__ float h2f(unsigned short b) { return (float)__builtin_bit_cast(_Float16, b); }
@@ -166,8 +169,8 @@ class Inlined:
 
 
 def input_params(nest: LoopNest, bufs: Buffers) -> list[str]:
-    params = [f"const {STORE_T[n.dtype]}* __restrict__ in{k}" for k, n in enumerate(nest.kernel.inputs)]
-    return params + [f"const {STORE_T[bufs.dtypes[name]]}* __restrict__ {name}" for name in bufs.extra]
+    params = [f"const {STORE_T[n.dtype]}* __restrict__ ALIGNED in{k}" for k, n in enumerate(nest.kernel.inputs)]
+    return params + [f"const {STORE_T[bufs.dtypes[name]]}* __restrict__ ALIGNED {name}" for name in bufs.extra]
 
 
 def render_index(index: Index, wide: bool) -> str:
@@ -460,7 +463,7 @@ def _vec_width(nest_shape: NestShape, bufs: Buffers, var: str, extent: int) -> i
 
 def signature(name: str, nest: LoopNest, out_dtype: DType, bufs: Buffers, extra: str = "") -> str:
     params = input_params(nest, bufs)
-    params.append(f"{STORE_T[out_dtype]}* __restrict__ out")
+    params.append(f"{STORE_T[out_dtype]}* __restrict__ ALIGNED out")
     if extra:
         params.append(extra)
     return f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}({", ".join(params)})'
@@ -477,27 +480,43 @@ def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned
     lines = [signature(nest.name, nest, out_dtype, bufs) + " {"]
     groups = cells // vec
     lines.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {groups}LL; g += (i64)gridDim.x * {THREADS}) {{")
-    # A masked load whose mask does not involve the stride-1 var is valid for the whole VEC run
-    # or for none of it: its pointer is chosen once per run (the buffer's start when masked, which
-    # is in bounds for VEC elements) and the run's loads are unconditional, so they merge into one
-    # vector load instead of VEC branches around 2-byte loads.
+    # Loads and the store that step through the stride-1 var take a pointer to the run's first
+    # element, set once per run, and index it by j_: the run is then visibly one 16-byte access
+    # (computed from the full index per element, the compiler split some runs into 2-, 4- and
+    # 8-byte pieces). A masked load whose mask does not involve the stride-1 var is valid for
+    # the whole run or for none of it: its pointer is the buffer's start when masked (in bounds
+    # for VEC elements) and the run's loads are unconditional, so they too merge into one vector
+    # load instead of VEC branches around 2-byte loads.
     runs: dict[str, list[str]] = {}
     pre: list[str] = []
+    store_run = None
     if shape.outer and vec > 1 and write.opcode is Opcode.STORE:
         sizes = {f"in{k}": math.prod(n.shape) for k, n in enumerate(nest.kernel.inputs)}
+
+        def first(index: Index) -> str:
+            at0 = Index(index.const, tuple((f"({inner_var}_b * {vec})" if v == inner_var else v, c) for v, c in index.terms))
+            return render_index(at0, True)
+
         for instr in shape.body:
             if instr.opcode is not Opcode.LOAD:
                 continue
             buf, index, valid = instr.arg
-            if buf in bufs.inline or not valid.bounds or any(b[0] == inner_var for b in valid.bounds):
+            if buf in bufs.inline or any(b[0] == inner_var for b in valid.bounds):
                 continue
             if dict(index.terms).get(inner_var) != 1 or sizes.get(buf, 0) < vec:
                 continue
             d, t, dt = instr.dest, VALUE_T[instr.value_type], bufs.dtypes[buf]
-            first = Index(index.const, tuple((f"({inner_var}_b * {vec})" if v == inner_var else v, c) for v, c in index.terms))
+            if not valid.bounds:
+                pre.append(f"    const {STORE_T[dt]}* {d}_p = {buf} + (i64)({first(index)});")
+                runs[d] = [f"const {t} {d} = ({t}){load_expr(dt, f'{d}_p[j_]')};"]
+                continue
             pre.append(f"    const bool {d}_ok = {valid.render()};")
-            pre.append(f"    const {STORE_T[dt]}* {d}_p = {buf} + ({d}_ok ? (i64)({render_index(first, True)}) : (i64)0);")
+            pre.append(f"    const {STORE_T[dt]}* {d}_p = {buf} + ({d}_ok ? (i64)({first(index)}) : (i64)0);")
             runs[d] = [f"const {t} {d}_raw = ({t}){load_expr(dt, f'{d}_p[j_]')};", f"const {t} {d} = {d}_ok ? {d}_raw : ({t})0;"]
+        out_index = write.arg[1]
+        if dict(out_index.terms).get(inner_var) == 1:
+            pre.append(f"    {STORE_T[out_dtype]}* out_p = out + (i64)({first(out_index)});")
+            store_run = f"      out_p[j_] = {store_expr(out_dtype, write.srcs[0])};"
     if shape.outer:
         base_vars = shape.outer[:-1] + [(inner_var + "_b", inner_extent // vec)]
         lines += decode(base_vars, "g", "    ", wide)
@@ -519,6 +538,8 @@ def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned
         if out_dtype is not int32:
             return plan_scatter(nest, shape, bufs)
         lines.append(f"      atomicAdd(&{buf}[{render_index(index, True)}], ({STORE_T[out_dtype]}){write.srcs[0]});")
+    elif store_run is not None:
+        lines.append(store_run)
     else:
         lines.append(f"      {buf}[{render_index(index, wide)}] = {store_expr(out_dtype, write.srcs[0])};")
     lines += ["    }", "  }", "}"]
@@ -612,7 +633,7 @@ def plan_scatter(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     params = input_params(nest, bufs)
 
     per = tile // THREADS  # occurrences per thread, held in registers as thread * per + e
-    sort = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {nest.name}_sort({", ".join(params + ["unsigned long long* __restrict__ runs"])}) {{']
+    sort = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {nest.name}_sort({", ".join(params + ["unsigned long long* __restrict__ ALIGNED runs"])}) {{']
     sort.append(f"  __shared__ unsigned long long s_[{tile}];")
     sort.append(f"  const i64 base_ = (i64)blockIdx.x * {tile};")
     sort.append("  const int th_ = threadIdx.x;")
@@ -672,7 +693,7 @@ def plan_scatter(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     sort.append(f"  for (int e_ = 0; e_ < {per}; e_++) runs[base_ + th_ * {per} + e_] = x_[e_];")
     sort.append("}")
 
-    acc = [f'extern "C" __global__ __launch_bounds__({block}) void {nest.name}({", ".join(params + ["const unsigned long long* __restrict__ runs", f"{acc_t}* __restrict__ out"])}) {{']
+    acc = [f'extern "C" __global__ __launch_bounds__({block}) void {nest.name}({", ".join(params + ["const unsigned long long* __restrict__ ALIGNED runs", f"{acc_t}* __restrict__ ALIGNED out"])}) {{']
     acc.append("#pragma clang fp contract(off)")
     acc.append("  __shared__ int lo_[64], start_[64];")
     acc.append(f"  __shared__ unsigned list_[{LIST_CAP}];")
@@ -889,7 +910,7 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     # split: partials then an ordered fold per cell
     part_name = nest.name + "_part"
     params = input_params(nest, bufs)
-    params.append(f"{acc_t}* __restrict__ scratch")
+    params.append(f"{acc_t}* __restrict__ ALIGNED scratch")
     lines = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {part_name}({", ".join(params)}) {{']
     lines.append(f"  const i64 g = blockIdx.x / {parts}, p_ = blockIdx.x % {parts};")
     lines += decode(shape.outer, "g", "  ", wide)
@@ -915,7 +936,7 @@ def fold_parts(name: str, shape: NestShape, acc_t: str, out_dtype: DType, out_re
     cell, its lanes folding parts lane, lane + 64, ... and a fixed butterfly folding the lanes,
     so a cell's chain of dependent loads is parts / 64 long instead of parts."""
     fold = shape.fold
-    lines = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}(const {acc_t}* __restrict__ scratch, {STORE_T[out_dtype]}* __restrict__ out) {{']
+    lines = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}(const {acc_t}* __restrict__ ALIGNED scratch, {STORE_T[out_dtype]}* __restrict__ ALIGNED out) {{']
     if parts <= 16:
         lines.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {cells}LL; g += (i64)gridDim.x * {THREADS}) {{")
         lines += decode(shape.outer, "g", "    ", wide)
@@ -965,7 +986,7 @@ def plan_columns(nest: LoopNest, shape: NestShape, bufs: Buffers, cells: int, R:
     body = ["      " + value_line(i, bufs) for i in shape.body]
     name = nest.name if parts == 1 else nest.name + "_part"
     params = input_params(nest, bufs)
-    params.append(f"{STORE_T[out_dtype]}* __restrict__ out" if parts == 1 else f"{acc_t}* __restrict__ scratch")
+    params.append(f"{STORE_T[out_dtype]}* __restrict__ ALIGNED out" if parts == 1 else f"{acc_t}* __restrict__ ALIGNED scratch")
     lines = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}({", ".join(params)}) {{']
     lines.append("  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;")
     lines.append(f"  const i64 tile = blockIdx.x / {parts}, p_ = blockIdx.x % {parts};")
