@@ -8,6 +8,12 @@
 // compute width; the 4 lanes of a row read 4 consecutive words and every row reads the same
 // streamed row, so reads are conflict-free broadcasts.
 //
+// With few resident rows per head the workgroups would be too few to fill the GPU and each row's
+// walk over the streamed rows one long chain of dependent steps: then (SPLIT = 4 or 8) a row is
+// held by SPLIT groups of LANES lanes, group g taking the streamed rows g, g + SPLIT, ... of
+// every tile, and the groups' partial results are combined at the end in a fixed butterfly
+// (the forward's as (max, total, accumulator) triples rescaled to the common max).
+//
 // This family carries the widths the MFMA kernels do not (f32 and f64 above all, where the
 // reference's tolerances are 1e-5 and 1e-12): it computes in the dtype's compute width with
 // natural exp/log, folding streamed rows in ascending order.
@@ -23,10 +29,12 @@
 namespace limn {
 namespace {
 
-constexpr int LANES = 4;                     // lanes per resident row
+constexpr int LANES = 4;                     // lanes per resident row and key group
 constexpr int THREADS = 256;                 // per workgroup
-constexpr int ROWS = THREADS / LANES;        // resident rows per workgroup
 constexpr int STREAM = 32;                   // streamed rows per LDS tile
+// resident rows per workgroup when each row's streamed rows are split among SPLIT groups of lanes
+template <int SPLIT>
+constexpr int rows_per_block() { return THREADS / (LANES * SPLIT); }
 
 template <typename C>
 __device__ __forceinline__ C exp_c(C x);
@@ -91,7 +99,25 @@ __device__ __forceinline__ typename T::Compute dot(const typename T::Compute* a,
   return row_sum(s);
 }
 
-template <typename T, int MAXD>
+// the sum of x over the SPLIT key groups of a row (every group gets the total): lanes of one
+// row's groups sit LANES apart
+template <int SPLIT, typename C>
+__device__ __forceinline__ C group_sum(C x) {
+  if (SPLIT > 1) x += __shfl_xor(x, LANES);
+  if (SPLIT > 2) x += __shfl_xor(x, 2 * LANES);
+  if (SPLIT > 4) x += __shfl_xor(x, 4 * LANES);
+  return x;
+}
+
+template <int SPLIT, typename C>
+__device__ __forceinline__ C group_max(C x) {
+  if (SPLIT > 1) x = fmax(x, __shfl_xor(x, LANES));
+  if (SPLIT > 2) x = fmax(x, __shfl_xor(x, 2 * LANES));
+  if (SPLIT > 4) x = fmax(x, __shfl_xor(x, 4 * LANES));
+  return x;
+}
+
+template <typename T, int MAXD, int SPLIT>
 __global__ __launch_bounds__(THREADS) void sdpa_fwd_rows(const typename T::Storage* __restrict__ q,
                                                          const typename T::Storage* __restrict__ k,
                                                          const typename T::Storage* __restrict__ v,
@@ -101,14 +127,14 @@ __global__ __launch_bounds__(THREADS) void sdpa_fwd_rows(const typename T::Stora
                                                          int64_t t_k, int hd, int hd_v, int causal,
                                                          typename T::Compute scale) {
   typedef typename T::Compute C;
-  constexpr int P = MAXD / LANES;
+  constexpr int P = MAXD / LANES, ROWS = rows_per_block<SPLIT>();
   __shared__ C Kt[STREAM][MAXD];
   __shared__ C Vt[STREAM][MAXD];
   __shared__ C Mt[STREAM];
   const int64_t chunks = (t_q + ROWS - 1) / ROWS;
   const int64_t b = blockIdx.x / chunks, chunk = blockIdx.x - b * chunks;
-  const int u = threadIdx.x % LANES;
-  const int64_t i = chunk * ROWS + threadIdx.x / LANES;
+  const int u = threadIdx.x % LANES, grp = (threadIdx.x / LANES) % SPLIT;
+  const int64_t i = chunk * ROWS + threadIdx.x / (LANES * SPLIT);
   const bool valid = i < t_q;
   C qv[P], acc[P];
   load_row<T, MAXD>(qv, q + b * t_q * hd, i, valid, hd, u);
@@ -126,7 +152,7 @@ __global__ __launch_bounds__(THREADS) void sdpa_fwd_rows(const typename T::Stora
     }
     __syncthreads();
     const int64_t end = r0 + STREAM < keys_end ? r0 + STREAM : keys_end;
-    for (int64_t j = r0; j < end; j++) {
+    for (int64_t j = r0 + grp; j < end; j += SPLIT) {
       const int lj = (int)(j - r0);
       if (mask != nullptr && Mt[lj] == C(0)) continue;
       const C s = dot<T, MAXD>(qv, Kt[lj], u) * scale;
@@ -144,13 +170,22 @@ __global__ __launch_bounds__(THREADS) void sdpa_fwd_rows(const typename T::Stora
     }
     __syncthreads();
   }
-  if (valid) {
+  if (SPLIT > 1) {
+    // the groups' totals rescaled to the row's max (a group that saw no visible key adds 0)
+    const C mr = group_max<SPLIT>(m);
+    const C f = m == -__builtin_inf() ? C(0) : exp_c<C>(m - mr);
+    l = group_sum<SPLIT>(l * f);
+#pragma unroll
+    for (int e = 0; e < P; e++) acc[e] = group_sum<SPLIT>(acc[e] * f);
+    m = mr;
+  }
+  if (valid && grp == 0) {
     store_row<T, MAXD>(out + b * t_q * hd_v, acc, i, hd_v, u, C(1) / l);
     if (u == 0) lse[b * t_q + i] = m + log_c<C>(l);
   }
 }
 
-template <typename T, int MAXD>
+template <typename T, int MAXD, int SPLIT>
 __global__ __launch_bounds__(THREADS) void sdpa_bwd_q_rows(
     const typename T::Storage* __restrict__ q, const typename T::Storage* __restrict__ k,
     const typename T::Storage* __restrict__ v, const typename T::Storage* __restrict__ dout,
@@ -158,14 +193,14 @@ __global__ __launch_bounds__(THREADS) void sdpa_bwd_q_rows(
     const typename T::Storage* __restrict__ mask, typename T::Storage* __restrict__ dq, int64_t t_q, int64_t t_k, int hd,
     int hd_v, int causal, typename T::Compute scale) {
   typedef typename T::Compute C;
-  constexpr int P = MAXD / LANES;
+  constexpr int P = MAXD / LANES, ROWS = rows_per_block<SPLIT>();
   __shared__ C Kt[STREAM][MAXD];
   __shared__ C Vt[STREAM][MAXD];
   __shared__ C Mt[STREAM];
   const int64_t chunks = (t_q + ROWS - 1) / ROWS;
   const int64_t b = blockIdx.x / chunks, chunk = blockIdx.x - b * chunks;
-  const int u = threadIdx.x % LANES;
-  const int64_t i = chunk * ROWS + threadIdx.x / LANES;
+  const int u = threadIdx.x % LANES, grp = (threadIdx.x / LANES) % SPLIT;
+  const int64_t i = chunk * ROWS + threadIdx.x / (LANES * SPLIT);
   const bool valid = i < t_q;
   C qv[P], ov[P], g[P];
   load_row<T, MAXD>(qv, q + b * t_q * hd, i, valid, hd, u);
@@ -185,7 +220,7 @@ __global__ __launch_bounds__(THREADS) void sdpa_bwd_q_rows(
     }
     __syncthreads();
     const int64_t end = r0 + STREAM < keys_end ? r0 + STREAM : keys_end;
-    for (int64_t j = r0; j < end; j++) {
+    for (int64_t j = r0 + grp; j < end; j += SPLIT) {
       const int lj = (int)(j - r0);
       if (mask != nullptr && Mt[lj] == C(0)) continue;
       const C s = dot<T, MAXD>(qv, Kt[lj], u);
@@ -197,10 +232,12 @@ __global__ __launch_bounds__(THREADS) void sdpa_bwd_q_rows(
     }
     __syncthreads();
   }
-  if (valid) store_row<T, MAXD>(dq + b * t_q * hd, g, i, hd, u, C(1));
+#pragma unroll
+  for (int e = 0; e < P; e++) g[e] = group_sum<SPLIT>(g[e]);
+  if (valid && grp == 0) store_row<T, MAXD>(dq + b * t_q * hd, g, i, hd, u, C(1));
 }
 
-template <typename T, int MAXD>
+template <typename T, int MAXD, int SPLIT>
 __global__ __launch_bounds__(THREADS) void sdpa_bwd_kv_rows(
     const typename T::Storage* __restrict__ q, const typename T::Storage* __restrict__ k,
     const typename T::Storage* __restrict__ v, const typename T::Storage* __restrict__ dout,
@@ -209,15 +246,15 @@ __global__ __launch_bounds__(THREADS) void sdpa_bwd_kv_rows(
     typename T::Storage* __restrict__ dv, int64_t t_q, int64_t t_k, int hd, int hd_v, int causal,
     typename T::Compute scale) {
   typedef typename T::Compute C;
-  constexpr int P = MAXD / LANES;
+  constexpr int P = MAXD / LANES, ROWS = rows_per_block<SPLIT>();
   __shared__ C Qt[STREAM][MAXD];
   __shared__ C Ot[STREAM][MAXD];
   __shared__ C Lt[STREAM];
   __shared__ C Dt[STREAM];
   const int64_t chunks = (t_k + ROWS - 1) / ROWS;
   const int64_t b = blockIdx.x / chunks, chunk = blockIdx.x - b * chunks;
-  const int u = threadIdx.x % LANES;
-  const int64_t j = chunk * ROWS + threadIdx.x / LANES;
+  const int u = threadIdx.x % LANES, grp = (threadIdx.x / LANES) % SPLIT;
+  const int64_t j = chunk * ROWS + threadIdx.x / (LANES * SPLIT);
   const bool valid = j < t_k;
   const bool live = valid && (mask == nullptr || T::load(mask, b * t_k + j) != C(0));
   C kv[P], vv[P], gk[P], gv[P];
@@ -228,8 +265,8 @@ __global__ __launch_bounds__(THREADS) void sdpa_bwd_kv_rows(
     gk[e] = C(0);
     gv[e] = C(0);
   }
-  // a causal key j is seen by queries i >= j only, so the block starts at its own first key
-  // (a multiple of ROWS, hence of STREAM); every thread meets the same barriers.
+  // a causal key j is seen by queries i >= j only, so the block starts at its own first key;
+  // every thread meets the same barriers.
   const int64_t first = causal ? chunk * ROWS : 0;
   const int64_t rows_end = live ? t_q : 0;
   for (int64_t r0 = first; r0 < t_q; r0 += STREAM) {
@@ -242,7 +279,11 @@ __global__ __launch_bounds__(THREADS) void sdpa_bwd_kv_rows(
     }
     __syncthreads();
     const int64_t end = r0 + STREAM < rows_end ? r0 + STREAM : rows_end;
-    for (int64_t i = (causal && j > r0) ? j : r0; i < end; i++) {
+    // this group's queries of the tile: r0 + grp, r0 + grp + SPLIT, ..., from the key's own
+    // position on under causality
+    int64_t from = r0 + grp;
+    if (causal && j > from) from += (j - from + SPLIT - 1) / SPLIT * SPLIT;
+    for (int64_t i = from; i < end; i += SPLIT) {
       const int li = (int)(i - r0);
       const C s = dot<T, MAXD>(kv, Qt[li], u);
       const C dp = dot<T, MAXD>(vv, Ot[li], u);
@@ -256,16 +297,22 @@ __global__ __launch_bounds__(THREADS) void sdpa_bwd_kv_rows(
     }
     __syncthreads();
   }
-  if (valid) {
+#pragma unroll
+  for (int e = 0; e < P; e++) {
+    gk[e] = group_sum<SPLIT>(gk[e]);
+    gv[e] = group_sum<SPLIT>(gv[e]);
+  }
+  if (valid && grp == 0) {
     store_row<T, MAXD>(dk + b * t_k * hd, gk, j, hd, u, C(1));
     store_row<T, MAXD>(dv + b * t_k * hd_v, gv, j, hd_v, u, C(1));
   }
 }
 
-template <typename T, int MAXD>
+template <typename T, int MAXD, int SPLIT>
 int launch_rows(SdpaPass pass, const SdpaArgs& a) {
   typedef typename T::Storage S;
   typedef typename T::Compute C;
+  constexpr int ROWS = rows_per_block<SPLIT>();
   const int64_t rows = pass == SDPA_BWD_KV ? a.t_k : a.t_q;
   const int64_t blocks = a.batch * ((rows + ROWS - 1) / ROWS);
   if (blocks > 0x7fffffff) return fail(LIMN_HIP_EUNSUPPORTED, "sdpa: %lld workgroups exceed one launch", (long long)blocks);
@@ -275,16 +322,16 @@ int launch_rows(SdpaPass pass, const SdpaArgs& a) {
   const S* mask = (const S*)a.mask;
   switch (pass) {
     case SDPA_FWD:
-      hipLaunchKernelGGL((sdpa_fwd_rows<T, MAXD>), grid, block, 0, a.stream, (const S*)a.q, (const S*)a.k, (const S*)a.v,
+      hipLaunchKernelGGL((sdpa_fwd_rows<T, MAXD, SPLIT>), grid, block, 0, a.stream, (const S*)a.q, (const S*)a.k, (const S*)a.v,
                          mask, (S*)a.out0, (C*)a.out1, a.t_q, a.t_k, hd, hd_v, causal, scale);
       break;
     case SDPA_BWD_Q:
-      hipLaunchKernelGGL((sdpa_bwd_q_rows<T, MAXD>), grid, block, 0, a.stream, (const S*)a.q, (const S*)a.k,
+      hipLaunchKernelGGL((sdpa_bwd_q_rows<T, MAXD, SPLIT>), grid, block, 0, a.stream, (const S*)a.q, (const S*)a.k,
                          (const S*)a.v, (const S*)a.dout, (const C*)a.lse, (const C*)a.delta, mask, (S*)a.out0, a.t_q,
                          a.t_k, hd, hd_v, causal, scale);
       break;
     case SDPA_BWD_KV:
-      hipLaunchKernelGGL((sdpa_bwd_kv_rows<T, MAXD>), grid, block, 0, a.stream, (const S*)a.q, (const S*)a.k,
+      hipLaunchKernelGGL((sdpa_bwd_kv_rows<T, MAXD, SPLIT>), grid, block, 0, a.stream, (const S*)a.q, (const S*)a.k,
                          (const S*)a.v, (const S*)a.dout, (const C*)a.lse, (const C*)a.delta, mask, (S*)a.out0,
                          (S*)a.out1, a.t_q, a.t_k, hd, hd_v, causal, scale);
       break;
@@ -292,13 +339,24 @@ int launch_rows(SdpaPass pass, const SdpaArgs& a) {
   return check_hip(hipGetLastError(), "launching an sdpa kernel");
 }
 
+// split each row's streamed rows among 4 or 8 groups of lanes when whole rows per lane group
+// would leave most CUs without a workgroup
+template <typename T, int MAXD>
+int launch_split(SdpaPass pass, const SdpaArgs& a) {
+  const int64_t rows = pass == SDPA_BWD_KV ? a.t_k : a.t_q;
+  const int64_t whole = a.batch * ((rows + rows_per_block<1>() - 1) / rows_per_block<1>());
+  if (whole < 256) return launch_rows<T, MAXD, 8>(pass, a);
+  if (whole < 1024) return launch_rows<T, MAXD, 4>(pass, a);
+  return launch_rows<T, MAXD, 1>(pass, a);
+}
+
 template <typename T>
 int launch_width(SdpaPass pass, const SdpaArgs& a) {
   const int64_t width = a.hd > a.hd_v ? a.hd : a.hd_v;
-  if (width <= 16) return launch_rows<T, 16>(pass, a);
-  if (width <= 64) return launch_rows<T, 64>(pass, a);
-  if (width <= 128) return launch_rows<T, 128>(pass, a);
-  return launch_rows<T, 256>(pass, a);
+  if (width <= 16) return launch_split<T, 16>(pass, a);
+  if (width <= 64) return launch_split<T, 64>(pass, a);
+  if (width <= 128) return launch_split<T, 128>(pass, a);
+  return launch_split<T, 256>(pass, a);
 }
 
 }  // namespace
