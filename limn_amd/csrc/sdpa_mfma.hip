@@ -1177,13 +1177,14 @@ __global__ __launch_bounds__(THREADS, 2) void sdpa_bwd_q_dma(const u16* __restri
 // ---------------------------------------------------------------------------------------------
 
 // Resident 32-row tiles per wave for each pass and head dim: 2 (each LDS operand read feeds two
-// MFMAs) wherever the accumulators still fit the register file.
+// MFMAs) only for the dK/dV pass at D = 64.
 template <int D>
 constexpr int tiles_per_wave(SdpaPass pass) {
-  // at D = 128 the forward and dQ pass run two workgroups per CU (two waves per SIMD), which
-  // hides their latency better than operand reuse; the dK/dV pass's four accumulator sets fill
-  // the register file at one tile
-  if (D == 128 || pass == SDPA_FWD) return 1;
+  // the forward and dQ pass run two workgroups per CU (two waves per SIMD), which hides their
+  // latency better than operand reuse (the D = 64 dQ pass of the GPT step: 448 -> 286 us per
+  // step at one tile); the dK/dV pass's four accumulator sets fill the register file at one
+  // tile when D = 128, and at D = 64 two tiles measured faster than one (650 against 687 us)
+  if (D == 128 || pass != SDPA_BWD_KV) return 1;
   return 2;
 }
 
