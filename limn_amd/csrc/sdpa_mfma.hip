@@ -504,7 +504,7 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_bwd_q_mfma(cons
 // ---------------------------------------------------------------------------------------------
 // dK/dV pass: resident key rows (NT tiles per wave), queries streaming 32 at a time.
 template <typename T, int D, int NT, bool CAUSAL, bool MASK>
-__global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_mfma(const u16* __restrict__ q, const u16* __restrict__ k,
+__global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_bwd_kv_mfma(const u16* __restrict__ q, const u16* __restrict__ k,
                                                                const u16* __restrict__ v, const u16* __restrict__ dout,
                                                                const float* __restrict__ lse,
                                                                const float* __restrict__ delta,
@@ -1176,16 +1176,14 @@ __global__ __launch_bounds__(THREADS, 2) void sdpa_bwd_q_dma(const u16* __restri
 
 // ---------------------------------------------------------------------------------------------
 
-// Resident 32-row tiles per wave for each pass and head dim: 2 (each LDS operand read feeds two
-// MFMAs) only for the dK/dV pass at D = 64.
+// Resident 32-row tiles per wave for each pass and head dim. The kernels take NT = 2 (each LDS
+// operand read feeds two MFMAs), but one tile per wave with two workgroups per CU (two waves per
+// SIMD) hides latency better wherever it fits: the D = 64 passes of the GPT step took 448 / 662
+// us per step (dQ / dK dV) at two tiles and 288 / 442 us at one; at D = 128 the dK/dV pass's
+// accumulators fill the register file at one tile (its LDS-DMA kernel, one workgroup per CU).
 template <int D>
-constexpr int tiles_per_wave(SdpaPass pass) {
-  // the forward and dQ pass run two workgroups per CU (two waves per SIMD), which hides their
-  // latency better than operand reuse (the D = 64 dQ pass of the GPT step: 448 -> 286 us per
-  // step at one tile); the dK/dV pass's four accumulator sets fill the register file at one
-  // tile when D = 128, and at D = 64 two tiles measured faster than one (650 against 687 us)
-  if (D == 128 || pass != SDPA_BWD_KV) return 1;
-  return 2;
+constexpr int tiles_per_wave(SdpaPass) {
+  return 1;
 }
 
 template <typename T, int D, int NT, bool CAUSAL, bool MASK, SdpaPass PASS>
