@@ -69,6 +69,7 @@ class HipDevice(CompiledDevice):
 
     def __init__(self) -> None:
         self.plan_kept: set | None = None  # set by plan_of for runners(), see there
+        self.plan_custom_inputs: set | None = None
         super().__init__()
         api = runtime.hip()
         assert api is not None, "construct via set_device('hip'), which explains what is missing"
@@ -200,11 +201,13 @@ class HipDevice(CompiledDevice):
         """The executor's plan_of, with the buffers that must hold their values recorded for
         runners(): the sinks and every CUSTOM src. runners() sees only the non-CUSTOM nests, and
         a contraction's epilogue may absorb a relu nest only when no one else reads the sum."""
-        self.plan_kept = {realized(s) for s in sinks} | {realized(src) for n in order if n.op is Op.CUSTOM for src in n.srcs}
+        self.plan_custom_inputs = {realized(src) for n in order if n.op is Op.CUSTOM for src in n.srcs}
+        self.plan_kept = {realized(s) for s in sinks} | self.plan_custom_inputs
         try:
             return super().plan_of(order, position, sinks)
         finally:
             self.plan_kept = None
+            self.plan_custom_inputs = None
 
     def runners(self, nests: list[LoopNest]) -> list[Runner]:
         from limn_amd.hip.emit import nest_runners

@@ -477,9 +477,9 @@ def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned
     inner_var, inner_extent = shape.outer[-1] if shape.outer else ("", 1)
     vec = _vec_width(shape, bufs, inner_var, inner_extent) if shape.outer and write.opcode is Opcode.STORE else 1
     wide = bufs.wide_index or cells > (1 << 30)
-    lines = [signature(nest.name, nest, out_dtype, bufs) + " {"]
+    lines = [signature(nest.name, nest, out_dtype, bufs) + " {", "  const i64 bid_ = blockIdx.x, nblk_ = gridDim.x;"]
     groups = cells // vec
-    lines.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {groups}LL; g += (i64)gridDim.x * {THREADS}) {{")
+    lines.append(f"  for (i64 g = bid_ * {THREADS} + threadIdx.x; g < {groups}LL; g += nblk_ * {THREADS}) {{")
     # Loads and the store that step through the stride-1 var take a pointer to the run's first
     # element, set once per run, and index it by j_: the run is then visibly one 16-byte access
     # (computed from the full index per element, the compiler split some runs into 2-, 4- and
@@ -544,7 +544,14 @@ def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned
         lines.append(f"      {buf}[{render_index(index, wide)}] = {store_expr(out_dtype, write.srcs[0])};")
     lines += ["    }", "  }", "}"]
     grid = max(1, min(-(-groups // THREADS), 1 << 20))
-    return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes={"elementwise": True})
+    notes: dict = {"elementwise": True}
+    if write.opcode is Opcode.STORE:
+        # the body between the block-index line and the closing brace, for merge_runs
+        notes["body"] = lines[2:-1]
+        notes["params"] = [(STORE_T[n.dtype], f"in{k}", True) for k, n in enumerate(nest.kernel.inputs)]
+        notes["params"] += [(STORE_T[bufs.dtypes[name]], name, True) for name in bufs.extra]
+        notes["params"].append((STORE_T[out_dtype], "out", False))
+    return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes=notes)
 
 
 SORT_TILE_LIMITS = ((1 << 16, 256), (1 << 20, 1024))  # occurrences -> occurrences per sorted tile
@@ -1235,10 +1242,94 @@ def inline_producers(nests: list[LoopNest], plans: list[Planned], kept: set | No
     return chosen
 
 
+MERGE_GRID = 2048  # the largest elementwise launch merged with its neighbours
+MERGE_MEMBERS = 16  # the most nests in one merged launch
+
+
+def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set | None, inlined: "InlineSet",
+               pairs: dict[int, int]) -> list[list[int]]:
+    """Groups of small elementwise nests that can share one launch, made at the place of the
+    group's last member. A member joins when it reads no other member's output (directly or
+    through an inlined producer); a nest between members that is not one may stay between them
+    if it reads no member's output either (it launches at its own place, before the group), and
+    one that does ends the group. No member's output is read by a CUSTOM call, which may sit
+    between nests. Each member is at most MERGE_GRID workgroups, a group at most MERGE_MEMBERS
+    nests. An optimizer step gives such groups across parameters (each parameter's moments, then
+    the parameter from the new moments, with the next parameter's gradient reduce between):
+    launches of a few microseconds each for the small parameters. `custom_inputs` None merges
+    nothing."""
+    if custom_inputs is None:
+        return []
+    fused = set(pairs) | set(pairs.values())
+
+    def reads(c: int) -> set:
+        nodes = set(nests[c].kernel.inputs)
+        for j in inlined.reached(nests[c]):
+            nodes |= set(nests[j].kernel.inputs)
+        return nodes
+
+    runs: list[list[int]] = []
+    run: list[int] = []
+    made: set = set()
+
+    def close() -> None:
+        if len(run) > 1:
+            runs.append(list(run))
+        run.clear()
+        made.clear()
+
+    for c, (nest, plan) in enumerate(zip(nests, plans)):
+        if c in inlined.producers:
+            continue  # launches nothing; its readers' reads() carry its inputs
+        ok = (
+            "body" in plan.notes
+            and c not in fused
+            and len(plan.launches) == 1
+            and plan.launches[0].grid <= MERGE_GRID
+            and nest.kernel.target not in custom_inputs
+        )
+        depends = bool(reads(c) & made)
+        if depends or len(run) >= MERGE_MEMBERS:
+            close()
+        if ok:
+            run.append(c)
+            made.add(nest.kernel.target)
+    close()
+    return runs
+
+
+def merged_source(name: str, nests: list[LoopNest], plans: list[Planned], run: list[int]) -> tuple[str, int]:
+    """One kernel for a run of elementwise nests: each member's body in its own block range, its
+    buffer names bound to its own parameters."""
+    params: list[str] = []
+    segments: list[str] = []
+    offset = 0
+    for s_, c in enumerate(run):
+        plan = plans[c]
+        grid = plan.launches[0].grid
+        binds = []
+        for ctype, pname, const in plan.notes["params"]:
+            q = "const " if const else ""
+            params.append(f"{q}{ctype}* __restrict__ ALIGNED s{s_}_{pname}")
+            binds.append(f"    {q}{ctype}* __restrict__ {pname} = ({q}{ctype}*)__builtin_assume_aligned(s{s_}_{pname}, 16);")
+        cond = f"blockIdx.x < {offset + grid}"
+        head = "  if" if s_ == 0 else "  } else if"
+        segments.append(f"{head} ({cond}) {{" if s_ < len(run) - 1 else ("  } else {" if s_ else "  {"))
+        segments += binds
+        segments.append(f"    const i64 bid_ = (i64)blockIdx.x - {offset}, nblk_ = {grid};")
+        segments += ["  " + ln for ln in plan.notes["body"]]
+        offset += grid
+    segments.append("  }")
+    source = f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}({", ".join(params)}) {{\n' + "\n".join(segments) + "\n}"
+    return source, offset
+
+
 def nest_runners(dev, nests: list[LoopNest]):
     """Compile every nest of a plan into one hipRTC program; one runner per nest, in order. A
     contraction whose only reader is a relu nest runs as one MFMA launch with a relu epilogue,
-    from the relu nest's runner (see epilogue_pairs)."""
+    from the relu nest's runner (see epilogue_pairs); small broadcast producers run inside their
+    readers (inline_producers); groups of small independent elementwise nests share one launch
+    from their last member's runner (merge_runs)."""
     plans = [plan_nest(n) for n in nests]
     kept = getattr(dev, "plan_kept", None)
     pairs = epilogue_pairs(nests, plans, kept)
@@ -1251,17 +1342,38 @@ def nest_runners(dev, nests: list[LoopNest]):
             plans[c] = plan_nest(nest, inlined)
     for j in inlined.producers:
         plans[j] = Planned("", [], notes={"inlined": True})
-    names = [launch.name for p in plans for launch in p.launches]
-    functions = runtime.load_functions(PRELUDE + "\n".join(p.source for p in plans), names) if names else {}
+    runs = merge_runs(nests, plans, getattr(dev, "plan_custom_inputs", None), inlined, pairs)
+    merged: dict[int, tuple[list[int], Launch]] = {}  # a run's last member -> (run, its launch)
+    merged_sources = []
+    for run in runs:
+        name = f"{nests[run[0]].name}_to_{nests[run[-1]].name}"
+        source, grid = merged_source(name, nests, plans, run)
+        merged_sources.append(source)
+        merged[run[-1]] = (run, Launch(name, grid, THREADS, "merged"))
+    in_run = {c for run in runs for c in run}
+    names = [launch.name for k, p in enumerate(plans) if k not in in_run for launch in p.launches]
+    names += [launch.name for _, launch in merged.values()]
+    kept_sources = [p.source for k, p in enumerate(plans) if k not in in_run]
+    functions = runtime.load_functions(PRELUDE + "\n".join(kept_sources + merged_sources), names) if names else {}
     runners = []
     operands: dict[int, list] = {}  # a fused contraction's inputs, from its call to its relu's
     producer_inputs: dict[int, list] = {}  # an inlined producer's inputs, from its call to its readers'
+    deferred: dict[int, tuple] = {}  # a merged run member's (inputs, outs), from its call to the run's launch
     for k, (nest, plan) in enumerate(zip(nests, plans)):
         if k in pairs:
             runners.append(_stash_runner(operands, k))
             continue
         if k in inlined.producers:
             runners.append(_keep_runner(producer_inputs, k))
+            continue
+        if k in merged:
+            run, launch = merged[k]
+            count = sum(len(plans[c].notes["params"]) for c in run)
+            runners.append(_merged_runner(_launcher(dev, functions[launch.name], launch, count - 1), run, nests, inlined,
+                                          producer_inputs, deferred, k))
+            continue
+        if k in in_run:
+            runners.append(_defer_runner(deferred, k))
             continue
         if k in fused:
             runners.append(_epilogue_runner(dev, plans[fused[k]].contraction, operands, fused[k]))
@@ -1277,6 +1389,35 @@ def nest_runners(dev, nests: list[LoopNest]):
             launchers.append((launch.args, _launcher(dev, functions[launch.name], launch, count - 1)))
         runners.append(_make_runner(dev, launchers, plan.scratch_bytes, extras, producer_inputs))
     return runners
+
+
+def _defer_runner(deferred: dict, k: int):
+    """A merged run's member before its last: keep its buffers for the run's one launch."""
+
+    def run(inputs: list, outs: list) -> None:
+        deferred[k] = (inputs, outs)
+
+    run.launches_nothing = True
+    return run
+
+
+def _merged_runner(launch, members: list[int], nests: list[LoopNest], inlined: "InlineSet", producer_inputs: dict,
+                   deferred: dict, k: int):
+    """A merged run's last member: one launch over every member's buffers, in parameter order
+    (inputs, an inlined producer's inputs, out)."""
+    extras = {c: inlined.extras(nests[c]) for c in members}
+
+    def run(inputs: list, outs: list) -> None:
+        deferred[k] = (inputs, outs)
+        ptrs: list[int] = []
+        for c in members:
+            ins, outs_c = deferred.pop(c)
+            ptrs += [b.ptr for b in ins]
+            ptrs += [producer_inputs[j][m].ptr for j, m in extras[c]]
+            ptrs.append(outs_c[0].ptr)
+        launch(ptrs)
+
+    return run
 
 
 def _keep_runner(producer_inputs: dict, k: int):

@@ -193,3 +193,49 @@ def test_a_load_masked_by_an_outer_dim_reads_whole_runs():
     nests, _ = lowered([inner * 2.0])
     source = emit.plan_nest(nests[-1]).source
     assert "_raw" not in source and "in0[" in source
+
+
+def runs_of(sinks: list[Tensor]):
+    nodes = [t.node for t in sinks]
+    order = topological(nodes)
+    nests = lower_all(nodes, order, schedule(nodes, order))
+    custom = {realized(src) for n in order if n.op is Op.CUSTOM for src in n.srcs}
+    kept = {realized(s) for s in nodes} | custom
+    plans = [emit.plan_nest(n) for n in nests]
+    pairs = emit.epilogue_pairs(nests, plans, kept)
+    inl = emit.InlineSet(nests, emit.inline_producers(nests, plans, kept, pairs))
+    return nests, emit.merge_runs(nests, plans, custom, inl, pairs)
+
+
+def test_independent_small_updates_share_a_launch():
+    """Moment updates of several parameters (as an optimizer step writes them): each reads only
+    old state and the gradient, so they form one group; an update that reads a new moment
+    starts a new group."""
+    params = [Tensor(rng.standard_normal((64,)).astype(np.float32)) for _ in range(3)]
+    grads = [Tensor(rng.standard_normal((64,)).astype(np.float32)) for _ in range(3)]
+    m = [p * 0.9 + g * 0.1 for p, g in zip(params, grads)]
+    nests, runs = runs_of(m)
+    assert [len(r) for r in runs] == [3]
+    newer = m[0] * 2.0 + 1.0  # reads a group member's output
+    nests, runs = runs_of(m + [newer])
+    members = {nests[c].kernel.target for r in runs for c in r}
+    assert realized(m[0].node) in members and all(
+        not (set(nests[c].kernel.inputs) & {nests[d].kernel.target for d in r}) for r in runs for c in r
+    )
+
+
+def test_nothing_merges_without_a_record_of_custom_inputs():
+    params = [Tensor(rng.standard_normal((64,)).astype(np.float32)) for _ in range(2)]
+    nests, _ = lowered([p * 2.0 for p in params])
+    plans = [emit.plan_nest(n) for n in nests]
+    assert emit.merge_runs(nests, plans, None, emit.InlineSet(nests, set()), {}) == []
+
+
+def test_merged_kernel_binds_each_members_buffers():
+    params = [Tensor(rng.standard_normal((64,)).astype(np.float32)) for _ in range(2)]
+    sinks = [p * 2.0 for p in params]
+    nests, runs = runs_of(sinks)
+    plans = [emit.plan_nest(n) for n in nests]
+    source, grid = emit.merged_source("merged", nests, plans, runs[0])
+    assert grid == sum(plans[c].launches[0].grid for c in runs[0])
+    assert "s0_in0" in source and "s1_out" in source and source.count("const i64 bid_") == 2

@@ -296,6 +296,35 @@ def test_commits_of_a_batch_run_as_one_copy(hipdev):
         np.testing.assert_array_equal(hipdev.copyout(t), w)
 
 
+def test_optimizer_style_updates_in_merged_launches(hipdev):
+    """Moments then parameters for several parameters, the way an optimizer step writes them:
+    the device launches each group of independent updates as one kernel (checked through the
+    recorded plan), and every committed value matches numpy."""
+    limn_device.active_device = hipdev
+    shapes = [(64,), (300, 7), (1000,), (48, 48)]
+    ps = [Tensor(randf(*sh)) for sh in shapes]
+    ms = [Tensor(randf(*sh)) for sh in shapes]
+    gs = [Tensor(randf(*sh)) for sh in shapes]
+    p_old, m_old, g_np = ([t.numpy().copy() for t in ts] for ts in (ps, ms, gs))
+    sinks = []
+    for p, m, g in zip(ps, ms, gs):
+        m_new = m * 0.9 + g * 0.1
+        m.assign(m_new)
+        p.assign(p - m_new * 0.01)
+        sinks += [m.node, p.node]
+    hipdev.record = []
+    bufs = hipdev.execute(sinks)
+    plan = hipdev.record[0].plan
+    hipdev.record = None
+    assert sum(1 for call in plan.calls if getattr(call.fn, "launches_nothing", False)) >= 3
+    for k in range(len(shapes)):
+        want_m = m_old[k] * np.float32(0.9) + g_np[k] * np.float32(0.1)
+        got_m = hipdev.copyout(bufs[2 * k]).view(np.float32).reshape(shapes[k])
+        got_p = hipdev.copyout(bufs[2 * k + 1]).view(np.float32).reshape(shapes[k])
+        np.testing.assert_allclose(got_m, want_m, rtol=1e-6, atol=1e-6)
+        np.testing.assert_allclose(got_p, p_old[k] - want_m * np.float32(0.01), rtol=1e-6, atol=1e-6)
+
+
 def test_assigns_commit_after_every_call(hipdev):
     """A training-style batch: three tensors assigned from expressions that read all three; every
     read sees the old values (reference tests/test_compiled_devices.py:73-98), and the commits land
