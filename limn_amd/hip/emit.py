@@ -469,6 +469,37 @@ def signature(name: str, nest: LoopNest, out_dtype: DType, bufs: Buffers, extra:
     return f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}({", ".join(params)})'
 
 
+def run_start(index: Index, var: str, vec: int) -> str:
+    """The index of a run's first element: `var` at `var`_b * vec."""
+    at0 = Index(index.const, tuple((f"({var}_b * {vec})" if v == var else v, c) for v, c in index.terms))
+    return render_index(at0, True)
+
+
+def run_loads(nest: LoopNest, body: list[Instr], bufs: Buffers, var: str, vec: int, indent: str) -> tuple[list[str], dict[str, list[str]]]:
+    """Pointers to the first element of each VEC run of the loads that step through `var` with
+    stride 1 (set before the j_ loop), and the lines that replace those loads inside it."""
+    sizes = {f"in{k}": math.prod(n.shape) for k, n in enumerate(nest.kernel.inputs)}
+    pre: list[str] = []
+    runs: dict[str, list[str]] = {}
+    for instr in body:
+        if instr.opcode is not Opcode.LOAD:
+            continue
+        buf, index, valid = instr.arg
+        if buf in bufs.inline or any(b[0] == var for b in valid.bounds):
+            continue
+        if dict(index.terms).get(var) != 1 or sizes.get(buf, 0) < vec:
+            continue
+        d, t, dt = instr.dest, VALUE_T[instr.value_type], bufs.dtypes[buf]
+        if not valid.bounds:
+            pre.append(f"{indent}const {STORE_T[dt]}* {d}_p = {buf} + (i64)({run_start(index, var, vec)});")
+            runs[d] = [f"const {t} {d} = ({t}){load_expr(dt, f'{d}_p[j_]')};"]
+            continue
+        pre.append(f"{indent}const bool {d}_ok = {valid.render()};")
+        pre.append(f"{indent}const {STORE_T[dt]}* {d}_p = {buf} + ({d}_ok ? (i64)({run_start(index, var, vec)}) : (i64)0);")
+        runs[d] = [f"const {t} {d}_raw = ({t}){load_expr(dt, f'{d}_p[j_]')};", f"const {t} {d} = {d}_ok ? {d}_raw : ({t})0;"]
+    return pre, runs
+
+
 def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     cells = math.prod(e for _, e in shape.outer)
     write = shape.write
@@ -491,31 +522,10 @@ def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned
     pre: list[str] = []
     store_run = None
     if shape.outer and vec > 1 and write.opcode is Opcode.STORE:
-        sizes = {f"in{k}": math.prod(n.shape) for k, n in enumerate(nest.kernel.inputs)}
-
-        def first(index: Index) -> str:
-            at0 = Index(index.const, tuple((f"({inner_var}_b * {vec})" if v == inner_var else v, c) for v, c in index.terms))
-            return render_index(at0, True)
-
-        for instr in shape.body:
-            if instr.opcode is not Opcode.LOAD:
-                continue
-            buf, index, valid = instr.arg
-            if buf in bufs.inline or any(b[0] == inner_var for b in valid.bounds):
-                continue
-            if dict(index.terms).get(inner_var) != 1 or sizes.get(buf, 0) < vec:
-                continue
-            d, t, dt = instr.dest, VALUE_T[instr.value_type], bufs.dtypes[buf]
-            if not valid.bounds:
-                pre.append(f"    const {STORE_T[dt]}* {d}_p = {buf} + (i64)({first(index)});")
-                runs[d] = [f"const {t} {d} = ({t}){load_expr(dt, f'{d}_p[j_]')};"]
-                continue
-            pre.append(f"    const bool {d}_ok = {valid.render()};")
-            pre.append(f"    const {STORE_T[dt]}* {d}_p = {buf} + ({d}_ok ? (i64)({first(index)}) : (i64)0);")
-            runs[d] = [f"const {t} {d}_raw = ({t}){load_expr(dt, f'{d}_p[j_]')};", f"const {t} {d} = {d}_ok ? {d}_raw : ({t})0;"]
+        pre, runs = run_loads(nest, shape.body, bufs, inner_var, vec, "    ")
         out_index = write.arg[1]
         if dict(out_index.terms).get(inner_var) == 1:
-            pre.append(f"    {STORE_T[out_dtype]}* out_p = out + (i64)({first(out_index)});")
+            pre.append(f"    {STORE_T[out_dtype]}* out_p = out + (i64)({run_start(out_index, inner_var, vec)});")
             store_run = f"      out_p[j_] = {store_expr(out_dtype, write.srcs[0])};"
     if shape.outer:
         base_vars = shape.outer[:-1] + [(inner_var + "_b", inner_extent // vec)]
@@ -974,10 +984,11 @@ COLUMN_BLOCKS = 2048  # workgroups a column reduce aims for (8 per CU): tiles x 
 def plan_columns(nest: LoopNest, shape: NestShape, bufs: Buffers, cells: int, R: int) -> Planned:
     """A reduce whose cells run along the stride-1 var and whose reduce vars are strided (a bias
     or LayerNorm-parameter gradient: a sum over every (batch, time) row of a (.., C) tensor).
-    A workgroup takes 64 consecutive cells, one per lane, so each row it reads is one coalesced
-    piece; its 4 waves take interleaved rows of one part of the reduce range; the parts, as many
-    as fill the machine, are partial totals in scratch folded per cell in order by a second
-    kernel (one part: written directly). Totals are deterministic."""
+    A lane takes VEC consecutive cells (16 bytes of the narrowest input), a workgroup 64 lanes'
+    worth, so each row it reads is one coalesced piece of whole-vector loads; its 4 waves take
+    interleaved rows of one part of the reduce range; the parts, as many as fill the machine, are
+    partial totals in scratch folded per cell in order by a second kernel (one part: written
+    directly). Totals are deterministic."""
     rdt = shape.reduce_dtype
     acc_dt = accumulate_in(rdt)
     acc_t = VALUE_T[acc_dt]
@@ -986,48 +997,66 @@ def plan_columns(nest: LoopNest, shape: NestShape, bufs: Buffers, cells: int, R:
     ident = literal(shape.identity, acc_dt)
     fold = shape.fold
     waves = THREADS // 64
-    tiles = -(-cells // COLUMN_TILE)
-    parts = max(1, min(-(-COLUMN_BLOCKS // tiles), R // (4 * waves)))
+    along, along_extent = shape.outer[-1]
+    vec = _vec_width(shape, bufs, along, along_extent)
+    per_tile = COLUMN_TILE * vec
+    tiles = -(-cells // per_tile)
+    # parts enough to fill the machine, each wave reading at least 16 rows of its part
+    parts = max(1, min(-(-COLUMN_BLOCKS // tiles), R // (16 * waves)))
     per_part = -(-R // parts)
     out_ref = f"out[{render_index(shape.out_index, wide)}]"
-    body = ["      " + value_line(i, bufs) for i in shape.body]
+    base_vars = shape.outer[:-1] + [(along + "_b", along_extent // vec)]
+    pre, runs = run_loads(nest, shape.body, bufs, along, vec, "        ") if vec > 1 else ([], {})
+    body = []
+    for instr in shape.body:
+        body += ["        " + ln for ln in runs[instr.dest]] if instr.dest in runs else ["        " + value_line(instr, bufs)]
     name = nest.name if parts == 1 else nest.name + "_part"
     params = input_params(nest, bufs)
     params.append(f"{STORE_T[out_dtype]}* __restrict__ ALIGNED out" if parts == 1 else f"{acc_t}* __restrict__ ALIGNED scratch")
     lines = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}({", ".join(params)}) {{']
     lines.append("  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;")
     lines.append(f"  const i64 tile = blockIdx.x / {parts}, p_ = blockIdx.x % {parts};")
-    lines.append(f"  const i64 g = tile * {COLUMN_TILE} + lane;")
-    lines.append(f"  {acc_t} acc = {ident};")
-    lines.append(f"  if (g < {cells}LL) {{")
-    lines += decode(shape.outer, "g", "    ", wide)
+    lines.append(f"  const i64 gb = tile * {COLUMN_TILE} + lane;  // the lane's run of {vec} cells")
+    lines.append(f"  {acc_t} acc[{vec}];")
+    lines.append("#pragma unroll")
+    lines.append(f"  for (int j_ = 0; j_ < {vec}; j_++) acc[j_] = {ident};")
+    lines.append(f"  if (gb < {cells // vec}LL) {{")
+    lines += decode(base_vars, "gb", "    ", wide)
     lines.append(f"    const i64 stop_ = (p_ + 1) * {per_part}LL < {R}LL ? (p_ + 1) * {per_part}LL : {R}LL;")
     lines.append(f"    for (i64 r_ = p_ * {per_part}LL + wave; r_ < stop_; r_ += {waves}) {{")
     lines += decode(shape.inner, "r_", "      ", True)
+    lines += pre
+    lines.append("#pragma unroll")
+    lines.append(f"      for (int j_ = 0; j_ < {vec}; j_++) {{")
+    lines.append(f"        const int {along} = {along}_b * {vec} + j_;")
     lines += body
-    lines.append("      " + _fold(fold, "acc", f"({acc_t}){shape.item}"))
-    lines += ["    }", "  }"]
-    # the waves' totals for each lane's cell, folded in wave order
-    lines.append(f"  __shared__ {acc_t} lds_[{waves}][64];")
-    lines.append("  lds_[wave][lane] = acc;")
+    lines.append("        " + _fold(fold, "acc[j_]", f"({acc_t}){shape.item}"))
+    lines += ["      }", "    }", "  }"]
+    # the waves' totals for each lane's cells, folded in wave order
+    lines.append(f"  __shared__ {acc_t} lds_[{waves}][{64 * vec}];")
+    lines.append("#pragma unroll")
+    lines.append(f"  for (int j_ = 0; j_ < {vec}; j_++) lds_[wave][lane * {vec} + j_] = acc[j_];")
     lines.append("  __syncthreads();")
-    lines.append(f"  if (wave == 0 && g < {cells}LL) {{")
-    lines.append("    acc = lds_[0][lane];")
+    lines.append(f"  if (wave == 0 && gb < {cells // vec}LL) {{")
+    lines.append("#pragma unroll")
+    lines.append(f"    for (int j_ = 0; j_ < {vec}; j_++) {{")
+    lines.append(f"      {acc_t} t = lds_[0][lane * {vec} + j_];")
     for w in range(1, waves):
-        lines.append("    " + _fold(fold, "acc", f"lds_[{w}][lane]"))
+        lines.append("      " + _fold(fold, "t", f"lds_[{w}][lane * {vec} + j_]"))
+    lines.append(f"      const i64 g = gb * {vec} + j_;")
     if parts == 1:
-        lines += decode(shape.outer, "g", "    ", wide)
-        lines.append(f"    {out_ref} = {store_expr(out_dtype, 'acc')};")
+        lines += decode(shape.outer, "g", "      ", wide)
+        lines.append(f"      {out_ref} = {store_expr(out_dtype, 't')};")
     else:
-        lines.append(f"    scratch[p_ * {cells}LL + g] = acc;  // [part][cell]: the final fold reads rows")
-    lines += ["  }", "}"]
+        lines.append(f"      scratch[p_ * {cells}LL + g] = t;  // [part][cell]: the final fold reads rows")
+    lines += ["    }", "  }", "}"]
     launches = [Launch(name, tiles * parts, THREADS, "io" if parts == 1 else "io_scratch")]
     if parts == 1:
-        return Planned("\n".join(lines), launches, notes={"columns": True, "parts": 1})
+        return Planned("\n".join(lines), launches, notes={"columns": True, "parts": 1, "vec": vec})
     final, final_grid = fold_parts(nest.name, shape, acc_t, out_dtype, out_ref, wide, cells, parts, ident, f"p_ * {cells}LL + g")
     launches.append(Launch(nest.name, final_grid, THREADS, "scratch_out"))
     return Planned("\n".join(lines) + "\n" + "\n".join(final), launches, scratch_bytes=cells * parts * acc_dt.itemsize,
-                   notes={"columns": True, "parts": parts})
+                   notes={"columns": True, "parts": parts, "vec": vec})
 
 
 def plan_nest(nest: LoopNest, inlined: "InlineSet | None" = None) -> Planned:

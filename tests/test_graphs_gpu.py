@@ -70,6 +70,17 @@ def test_concatenation_by_pads_loads_whole_runs(hipdev, dtype):
     check(hipdev, stacked, exact=True)
 
 
+@pytest.mark.parametrize("shape,dtype", [((256, 96), bfloat16), ((4000, 36), float32), ((500, 37), float32), ((3, 700, 24), float32)],
+                         ids=["bf16-runs-of-8", "f32-runs-of-4", "odd-width", "two-reduce-axes"])
+def test_column_reduces_take_runs_of_cells(hipdev, shape, dtype):
+    """Sums and maxes down the columns (a bias gradient's shape): a lane takes 16 bytes of
+    consecutive columns when the width allows."""
+    x = Tensor(randf(*shape), dtype=dtype)
+    axes = tuple(range(len(shape) - 1))
+    check(hipdev, x.cast(float32).sum(axis=axes), worst=1e-5)
+    check(hipdev, x.max(axis=axes), exact=True)
+
+
 def test_max_propagates_nan(hipdev):
     data = rng.standard_normal((4, 5000)).astype(np.float32)
     data[1, 4321] = np.nan
