@@ -469,8 +469,34 @@ LIMN_DMA_LAYOUT(F16, 128)
 // store at c's strides.
 template <typename T, int EPI>
 __global__ __launch_bounds__(256) void matmul_splits(const float* __restrict__ ws, u16* __restrict__ c, MatmulShape s,
-                                                     int64_t split) {
+                                                     int64_t split, int quad) {
   const int64_t total = s.batch * s.M * s.N;
+  if (quad) {
+    // 4 consecutive n per thread (N % 4 == 0, output rows contiguous and 8-byte aligned): one
+    // 16-byte load per slice, the row and column found once, one 8-byte store; each element's
+    // slices are still added in slice order
+    for (int64_t i = (blockIdx.x * (int64_t)256 + threadIdx.x) * 4; i < total; i += (int64_t)gridDim.x * 1024) {
+      float4 v = *(const float4*)(ws + i);
+      for (int64_t k = 1; k < split; k++) {
+        const float4 w = *(const float4*)(ws + k * total + i);
+        v.x += w.x;
+        v.y += w.y;
+        v.z += w.z;
+        v.w += w.w;
+      }
+      if (EPI == MATMUL_EPILOGUE_RELU) {
+        v.x = v.x > 0.f ? v.x : 0.f;
+        v.y = v.y > 0.f ? v.y : 0.f;
+        v.z = v.z > 0.f ? v.z : 0.f;
+        v.w = v.w > 0.f ? v.w : 0.f;
+      }
+      const int64_t col = i % s.N, row = (i / s.N) % s.M, bz = i / (s.N * s.M);
+      const uint2 packed = {(unsigned)T::pack(v.x) | ((unsigned)T::pack(v.y) << 16),
+                            (unsigned)T::pack(v.z) | ((unsigned)T::pack(v.w) << 16)};
+      *(uint2*)(c + bz * s.c_batch + row * s.c_m + col) = packed;
+    }
+    return;
+  }
   for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
     float v = ws[i];
     for (int64_t k = 1; k < split; k++) v += ws[k * total + i];
@@ -510,9 +536,11 @@ int launch_tile(const void* a, const void* b, void* c, const MatmulShape& s, con
   const int rc = check_hip(hipGetLastError(), "launching the split matmul kernel");
   if (rc != LIMN_HIP_OK) return rc;
   const int64_t total = s.batch * s.M * s.N;
-  const int64_t fold_blocks = (total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096;
+  const bool quad = s.N % 4 == 0 && s.c_n == 1 && s.c_m % 4 == 0 && s.c_batch % 4 == 0 && (uintptr_t)c % 8 == 0;
+  const int64_t per_thread = quad ? 4 : 1, threads = (total + per_thread - 1) / per_thread;
+  const int64_t fold_blocks = (threads + 255) / 256 < 4096 ? (threads + 255) / 256 : 4096;
   hipLaunchKernelGGL((matmul_splits<T, EPI>), dim3((unsigned)fold_blocks), dim3(256), 0, stream, (const float*)ws,
-                     (u16*)c, s, plan.split);
+                     (u16*)c, s, plan.split, (int)quad);
   return check_hip(hipGetLastError(), "launching the matmul slice fold");
 }
 
