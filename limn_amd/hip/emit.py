@@ -1271,7 +1271,8 @@ def inline_producers(nests: list[LoopNest], plans: list[Planned], kept: set | No
     return chosen
 
 
-MERGE_GRID = 2048  # the largest elementwise launch merged with its neighbours
+MERGE_GRID = 1 << 16  # the largest elementwise launch merged with its neighbours
+MERGE_GROUP_GRID = 1 << 20  # the most workgroups of one merged launch
 MERGE_MEMBERS = 16  # the most nests in one merged launch
 
 
@@ -1283,7 +1284,7 @@ def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set |
     if it reads no member's output either (it launches at its own place, before the group), and
     one that does ends the group. No member's output is read by a CUSTOM call, which may sit
     between nests. Each member is at most MERGE_GRID workgroups, a group at most MERGE_MEMBERS
-    nests. An optimizer step gives such groups across parameters (each parameter's moments, then
+    nests and MERGE_GROUP_GRID workgroups. An optimizer step gives such groups across parameters (each parameter's moments, then
     the parameter from the new moments, with the next parameter's gradient reduce between):
     launches of a few microseconds each for the small parameters. `custom_inputs` None merges
     nothing."""
@@ -1318,7 +1319,8 @@ def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set |
             and nest.kernel.target not in custom_inputs
         )
         depends = bool(reads(c) & made)
-        if depends or len(run) >= MERGE_MEMBERS:
+        grid = plan.launches[0].grid if ok else 0
+        if depends or len(run) >= MERGE_MEMBERS or sum(plans[m].launches[0].grid for m in run) + grid > MERGE_GROUP_GRID:
             close()
         if ok:
             run.append(c)
