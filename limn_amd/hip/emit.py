@@ -788,6 +788,16 @@ def stride_one_var(nest: LoopNest, shape: NestShape) -> str | None:
     return max(weight, key=lambda v: weight[v])
 
 
+def mergeable(nest: LoopNest, bufs: Buffers, lines: list[str], notes: dict) -> dict:
+    """A single-launch kernel's notes plus what merge_runs needs to place it in a merged launch:
+    its body (after the block-index line, before the closing brace) and its parameters."""
+    out_dtype = nest.kernel.target.dtype
+    params = [(STORE_T[n.dtype], f"in{k}", True) for k, n in enumerate(nest.kernel.inputs)]
+    params += [(STORE_T[bufs.dtypes[name]], name, True) for name in bufs.extra]
+    params.append((STORE_T[out_dtype], "out", False))
+    return {**notes, "body": lines[2:-1], "params": params}
+
+
 def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     cells = math.prod(e for _, e in shape.outer)
     R = math.prod(e for _, e in shape.inner)
@@ -829,8 +839,8 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     inner_var, inner_extent = shape.inner[-1]
 
     if group == 1:
-        lines = [signature(nest.name, nest, out_dtype, bufs) + " {"]
-        lines.append(f"  for (i64 g = blockIdx.x * (i64){THREADS} + threadIdx.x; g < {cells}LL; g += (i64)gridDim.x * {THREADS}) {{")
+        lines = [signature(nest.name, nest, out_dtype, bufs) + " {", "  const i64 bid_ = blockIdx.x, nblk_ = gridDim.x;"]
+        lines.append(f"  for (i64 g = bid_ * {THREADS} + threadIdx.x; g < {cells}LL; g += nblk_ * {THREADS}) {{")
         lines += decode(shape.outer, "g", "    ", wide)
         lines.append(f"    {acc_t} acc = {ident};")
         for var, extent in shape.inner:
@@ -841,7 +851,7 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
         lines.append(f"    {out_ref} = {store_expr(out_dtype, 'acc')};")
         lines += ["  }", "}"]
         grid = max(1, min(-(-cells // THREADS), 1 << 20))
-        return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes={"group": 1})
+        return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes=mergeable(nest, bufs, lines, {"group": 1}))
 
     vec = _vec_width(shape, bufs, inner_var, inner_extent)
     chunks = R // vec  # vec divides the innermost extent, hence R
@@ -868,9 +878,9 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
         while G < chunks:
             G *= 2
         per_wave = 64 // G
-        lines = [signature(nest.name, nest, out_dtype, bufs) + " {"]
+        lines = [signature(nest.name, nest, out_dtype, bufs) + " {", "  const i64 bid_ = blockIdx.x, nblk_ = gridDim.x;"]
         lines.append(f"  const int lane = threadIdx.x & 63, sub_ = lane % {G};")
-        lines.append(f"  for (i64 g0 = (blockIdx.x * (i64){waves} + (threadIdx.x >> 6)) * {per_wave}; g0 < {cells}LL; g0 += (i64)gridDim.x * {waves * per_wave}) {{")
+        lines.append(f"  for (i64 g0 = (bid_ * {waves} + (threadIdx.x >> 6)) * {per_wave}; g0 < {cells}LL; g0 += nblk_ * {waves * per_wave}) {{")
         lines.append(f"    const i64 g = g0 + lane / {G};")
         lines.append(f"    {acc_t} acc = {ident};")
         lines.append(f"    if (g < {cells}LL) {{")
@@ -887,11 +897,11 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
         lines.append(f"      {out_ref} = {store_expr(out_dtype, 'acc')};")
         lines += ["    }", "  }", "}"]
         grid = max(1, min(-(-cells // (waves * per_wave)), 1 << 20))
-        return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes={"group": G, "vec": vec})
+        return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes=mergeable(nest, bufs, lines, {"group": G, "vec": vec}))
     if group == 64:
-        lines = [signature(nest.name, nest, out_dtype, bufs) + " {"]
+        lines = [signature(nest.name, nest, out_dtype, bufs) + " {", "  const i64 bid_ = blockIdx.x, nblk_ = gridDim.x;"]
         lines.append("  const int lane = threadIdx.x & 63;")
-        lines.append(f"  for (i64 g = blockIdx.x * (i64){waves} + (threadIdx.x >> 6); g < {cells}LL; g += (i64)gridDim.x * {waves}) {{")
+        lines.append(f"  for (i64 g = bid_ * {waves} + (threadIdx.x >> 6); g < {cells}LL; g += nblk_ * {waves}) {{")
         lines += decode(shape.outer, "g", "    ", wide)
         lines.append(f"    {acc_t} acc = {ident};")
         lines += strided_loop("lane", f"{chunks}LL", 64)
@@ -899,7 +909,7 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
         lines.append(f"    if (lane == 0) {out_ref} = {store_expr(out_dtype, 'acc')};")
         lines += ["  }", "}"]
         grid = max(1, min(-(-cells // waves), 1 << 20))
-        return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes={"group": 64, "vec": vec})
+        return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes=mergeable(nest, bufs, lines, {"group": 64, "vec": vec}))
 
     # a workgroup per (cell, part)
     def block_fold(lines: list[str]) -> None:
@@ -913,8 +923,8 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
             lines.append("      " + _fold(fold, "acc", f"lds_[{w}]"))
 
     if parts == 1:
-        lines = [signature(nest.name, nest, out_dtype, bufs) + " {"]
-        lines.append(f"  for (i64 g = blockIdx.x; g < {cells}LL; g += gridDim.x) {{")
+        lines = [signature(nest.name, nest, out_dtype, bufs) + " {", "  const i64 bid_ = blockIdx.x, nblk_ = gridDim.x;"]
+        lines.append(f"  for (i64 g = bid_; g < {cells}LL; g += nblk_) {{")
         lines += decode(shape.outer, "g", "    ", wide)
         lines.append(f"    {acc_t} acc = {ident};")
         lines += strided_loop("threadIdx.x", f"{chunks}LL", THREADS)
@@ -922,7 +932,7 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
         lines.append(f"      {out_ref} = {store_expr(out_dtype, 'acc')};")
         lines += ["    }", "    __syncthreads();", "  }", "}"]
         grid = max(1, min(cells, 1 << 20))
-        return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes={"group": THREADS, "vec": vec})
+        return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes=mergeable(nest, bufs, lines, {"group": THREADS, "vec": vec}))
 
     # split: partials then an ordered fold per cell
     part_name = nest.name + "_part"

@@ -336,6 +336,16 @@ def test_optimizer_style_updates_in_merged_launches(hipdev):
         np.testing.assert_allclose(got_p, p_old[k] - want_m * np.float32(0.01), rtol=1e-6, atol=1e-6)
 
 
+def test_independent_reduces_of_every_form_in_one_launch(hipdev):
+    """Four independent row reductions, one of each single-launch form (a thread, a lane group, a
+    wave and a workgroup per cell), share one merged launch and match the oracle."""
+    xs = [Tensor(randf(100, 30)), Tensor(randf(200, 64)), Tensor(randf(50, 1000)), Tensor(randf(8, 5000))]
+    sums = [x.sum(axis=1) for x in xs]
+    assert launch_free_calls(hipdev, [t.node for t in sums]) == 3
+    for t in sums:
+        check(hipdev, t, rtol=1e-4, atol=1e-4)
+
+
 def test_assigns_commit_after_every_call(hipdev):
     """A training-style batch: three tensors assigned from expressions that read all three; every
     read sees the old values (reference tests/test_compiled_devices.py:73-98), and the commits land
