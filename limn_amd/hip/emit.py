@@ -642,7 +642,6 @@ def plan_scatter(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
         raise NotImplementedError("a scatter row index that depends on the column")
     value_body = _needed(shape.body, {write.srcs[0]})
     acc_t = STORE_T[out_dtype]
-    wide = bufs.wide_index
     tile = next((t for limit, t in SORT_TILE_LIMITS if occurrences <= limit), SORT_TILE_MAX)
     tiles = max(1, -(-occurrences // tile))
     block = 64  # one wave: the scan and the tile search below are lane-wide

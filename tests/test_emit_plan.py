@@ -150,7 +150,7 @@ def test_a_producer_read_by_a_contraction_runs():
 def test_a_gathered_table_is_not_inlined():
     table = Tensor(rng.standard_normal((16, 4)).astype(np.float32)) * 3.0
     idx = Tensor(rng.integers(0, 16, size=(5,)).astype(np.int32))
-    nests, chosen = inlined_of([table.gather_rows(idx)])
+    _, chosen = inlined_of([table.gather_rows(idx)])
     assert chosen == set()
 
 
