@@ -9,8 +9,8 @@
 // streamed row, so reads are conflict-free broadcasts.
 //
 // With few resident rows per head the workgroups would be too few to fill the GPU and each row's
-// walk over the streamed rows one long chain of dependent steps: then (SPLIT = 4 or 8) a row is
-// held by SPLIT groups of LANES lanes, group g taking the streamed rows g, g + SPLIT, ... of
+// walk over the streamed rows one long chain of dependent steps: then (SPLIT = 4, 8 or 16) a row
+// is held by SPLIT groups of LANES lanes, group g taking the streamed rows g, g + SPLIT, ... of
 // every tile, and the groups' partial results are combined at the end in a fixed butterfly
 // (the forward's as (max, total, accumulator) triples rescaled to the common max).
 //
@@ -106,6 +106,7 @@ __device__ __forceinline__ C group_sum(C x) {
   if (SPLIT > 1) x += __shfl_xor(x, LANES);
   if (SPLIT > 2) x += __shfl_xor(x, 2 * LANES);
   if (SPLIT > 4) x += __shfl_xor(x, 4 * LANES);
+  if (SPLIT > 8) x += __shfl_xor(x, 8 * LANES);
   return x;
 }
 
@@ -114,6 +115,7 @@ __device__ __forceinline__ C group_max(C x) {
   if (SPLIT > 1) x = fmax(x, __shfl_xor(x, LANES));
   if (SPLIT > 2) x = fmax(x, __shfl_xor(x, 2 * LANES));
   if (SPLIT > 4) x = fmax(x, __shfl_xor(x, 4 * LANES));
+  if (SPLIT > 8) x = fmax(x, __shfl_xor(x, 8 * LANES));
   return x;
 }
 
@@ -339,12 +341,13 @@ int launch_rows(SdpaPass pass, const SdpaArgs& a) {
   return check_hip(hipGetLastError(), "launching an sdpa kernel");
 }
 
-// split each row's streamed rows among 4 or 8 groups of lanes when whole rows per lane group
-// would leave most CUs without a workgroup
+// split each row's streamed rows among 4, 8 or 16 groups of lanes when whole rows per lane
+// group would leave most CUs without a workgroup
 template <typename T, int MAXD>
 int launch_split(SdpaPass pass, const SdpaArgs& a) {
   const int64_t rows = pass == SDPA_BWD_KV ? a.t_k : a.t_q;
   const int64_t whole = a.batch * ((rows + rows_per_block<1>() - 1) / rows_per_block<1>());
+  if (whole < 64) return launch_rows<T, MAXD, 16>(pass, a);
   if (whole < 256) return launch_rows<T, MAXD, 8>(pass, a);
   if (whole < 1024) return launch_rows<T, MAXD, 4>(pass, a);
   return launch_rows<T, MAXD, 1>(pass, a);

@@ -103,13 +103,13 @@ def test_rows_family_matches_the_oracle(hipdev, case, causal, dtype_name):
 
 @pytest.mark.parametrize(
     "shapes",
-    [((24, 700, 16), (24, 700, 16), (24, 700, 16)), ((64, 1100, 8), (64, 1100, 8), (64, 1100, 8))],
-    ids=["four-groups", "whole-rows"],
+    [((70, 60, 16), (70, 60, 16), (70, 60, 16)), ((24, 700, 16), (24, 700, 16), (24, 700, 16)), ((64, 1100, 8), (64, 1100, 8), (64, 1100, 8))],
+    ids=["eight-groups", "four-groups", "whole-rows"],
 )
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 def test_rows_family_lane_group_splits(hipdev, shapes, causal):
-    """The small cases above split each row's keys among 8 lane groups; 24 heads of 700 rows
-    take 4 groups, 64 heads of 1100 rows whole rows per group."""
+    """The small cases above split each row's keys among 16 lane groups; 70 heads of 60 rows take
+    8, 24 heads of 700 rows 4, 64 heads of 1100 rows whole rows per group."""
     check_case(hipdev, 6, shapes, causal, "float32")
 
 
