@@ -138,7 +138,7 @@ def c_device_run(build) -> float:
     """Seconds spent inside the compiled nests when the graph `build()` returns (a list of
     tensors) is realized on the CPU baseline: oracle/c_device.py, limn's single-threaded C backend
     restated over this package's IR. Plan building and compiling are not timed."""
-    from limn_amd import device as limn_device
+    from limn_amd.seam import device as limn_device
     from oracle.c_device import CDevice
 
     saved = limn_device.active_device
@@ -157,7 +157,7 @@ def c4_cpu_baseline(host, scale: float, B: int, H: int, units: float) -> dict:
     the reference's): limn's composed causal attention, forward and backward through the Tensor
     API, as the reference's C backend runs it (no CUSTOM kernels). Scaled to all B*H pairs."""
     from limn_amd.dtypes import bf16_values
-    from limn_amd.tensor import Tensor, grad
+    from limn_amd.seam import Tensor, grad
 
     q, k, v, do = (bf16_values(h.reshape(B, H, -1, h.shape[-1])[:1, :1]).astype(np.float32) for h in host)
 
@@ -238,8 +238,8 @@ def bench_c2(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     emitted by the hip device, which evaluates the six per-row and scalar kernels inside their
     readers (5 launches). Reports the chain's algorithmic GB/s, timed from its first call to the
     end of its last, and each launched kernel's."""
-    from limn_amd import device as limn_device
-    from limn_amd.tensor import Tensor
+    from limn_amd.seam import device as limn_device
+    from limn_amd.seam import Tensor
 
     N = 8192
     limn_device.active_device = dev
@@ -336,10 +336,10 @@ def bench_c3(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     store; A, B ~ N(0, 0.125^2) from default_rng(3). The scheduler gives two nests (the SUM
     contraction and the relu); the device runs the pair as one MFMA launch with the relu in its
     store, the sum's call launching nothing. Both calls are timed."""
-    from limn_amd import device as limn_device
+    from limn_amd.seam import device as limn_device
     from limn_amd.dtypes import bf16_bits, bf16_values
-    from limn_amd.ops import bfloat16
-    from limn_amd.tensor import Tensor
+    from limn_amd.seam import bfloat16
+    from limn_amd.seam import Tensor
 
     n = 4096
     r = np.random.default_rng(3)
@@ -404,8 +404,8 @@ def bench_c1(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     default_rng(1), scale 1/8; one step is the forward and both backward passes (the general-width
     kernels: f32 has no MFMA path). Launch-latency bound: reported in microseconds and as
     FlashAttention-convention flop/s against the f32 peak."""
-    from limn_amd.ops import Node, Op, custom, float32
-    from limn_amd.tensor import Tensor, grad
+    from limn_amd.seam import Node, Op, custom, float32
+    from limn_amd.seam import Tensor, grad
 
     B, H, S, D = 2, 4, 256, 64
     scale = D**-0.5
@@ -480,14 +480,14 @@ def bench_c5(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     """one training step of the byte-level GPT (vocab 256, d 512, 8 layers,
     8 heads, ctx 512, batch 32, tanh GELU, bf16 activations over float32 masters, AdamW lr 3e-4
     wd 0.1), random init from seed 5, tokens uniform in [0, 256) from default_rng(5). The step is
-    captured (limn_amd.capture) and replayed; a step is forward, backward and the AdamW update
+    captured (limn's capture) and replayed; a step is forward, backward and the AdamW update
     committed with the loss, one plan transaction ending in one device synchronize, so wall time
     around K replays is the whole job's (kernel time plus host launch time)."""
-    from limn_amd import device as limn_device
-    from limn_amd.capture import capture
+    from limn_amd.seam import device as limn_device
+    from limn_amd.seam import capture
     from limn_amd.gpt import GPTConfig, make_trainer, synthetic_batch
-    from limn_amd.ops import float32
-    from limn_amd.tensor import set_seed
+    from limn_amd.seam import float32
+    from limn_amd.seam import set_seed
 
     cfg = GPTConfig()
     saved = limn_device.active_device
@@ -515,7 +515,7 @@ def bench_c5(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
 
     cpu = None
     if with_cpu:
-        from limn_amd import device as limn_device2
+        from limn_amd.seam import device as limn_device2
         from oracle.c_device import CDevice
 
         twin = GPTConfig(batch=1, dtype=float32)
@@ -583,7 +583,7 @@ def main() -> int:
     from limn_amd.dtypes import bf16_bits, bf16_values
     from limn_amd.hip.device import HipDevice
     from limn_amd.hip.runtime import hip_unavailable
-    from limn_amd.ops import Node, Op, bfloat16, custom, float32
+    from limn_amd.seam import Node, Op, bfloat16, custom, float32
 
     reason = hip_unavailable()
     if reason is not None:

@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from limn_amd.ops import DType, bfloat16, float16, float32, float64, int8, int16, int32
+from limn_amd.seam import DType, bfloat16, float16, float32, float64, int8, int16, int32
 
 STORAGE: dict[DType, np.dtype] = {
     float64: np.dtype(np.float64),
@@ -46,7 +46,7 @@ def bf16_values(bits: np.ndarray) -> np.ndarray:
 def to_storage(data, dtype: DType) -> np.ndarray:
     """Any array-like as `dtype`'s host storage (C-contiguous)."""
     array = np.asarray(data)
-    if dtype is bfloat16:
+    if dtype == bfloat16:
         if array.dtype == np.uint16:  # already bit patterns
             return np.ascontiguousarray(array)
         return bf16_bits(array.astype(np.float32))
@@ -56,4 +56,4 @@ def to_storage(data, dtype: DType) -> np.ndarray:
 def from_storage(raw: np.ndarray, dtype: DType, shape: tuple[int, ...]) -> np.ndarray:
     """A device's flat bytes as numbers of `dtype` (bfloat16 widened to float32)."""
     arr = np.asarray(raw).view(STORAGE[dtype]).reshape(shape)
-    return bf16_values(arr) if dtype is bfloat16 else arr
+    return bf16_values(arr) if dtype == bfloat16 else arr

@@ -1,4 +1,4 @@
-"""The C5 workload: one training step of a byte-level GPT built from limn_amd.nn.
+"""The C5 workload: one training step of a byte-level GPT built from limn's nn layers.
 
 The model follows reference examples/train_stories.py:23-58 (pre-norm blocks: fused qkv Linear,
 causal attention through limn's CUSTOM seam, output projection, MLP 4x; token + position
@@ -7,7 +7,11 @@ vocab 256, d_model 512, 8 layers, 8 heads (head dim 64), context 512, batch 32, 
 GELU, AdamW (lr 3e-4, weight decay 0.1).
 
 The residual stream (and its gradient) is materialized after every sublayer; see
-`materialized`.
+`materialized`. limn has no GELU (its examples use relu), so `gelu` here composes the tanh
+form from primitives.
+
+Everything limn-facing comes through limn_amd.seam: with limn importable this is a model on
+limn's own Tensor, nn and AdamW.
 
 Mixed precision, explicit in the graph: parameters (and AdamW's state) stay float32 masters;
 each Linear casts its weight and bias to the activation dtype at use, so the products run as
@@ -19,14 +23,28 @@ attention are bf16. The backward of each cast hands float32 gradients to the mas
 
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass
 
 import numpy as np
 
-from limn_amd.nn import Embedding, LayerNorm, Linear, gelu, parameters
-from limn_amd.ops import DType, Node, Op, bfloat16, float32, int32
-from limn_amd.optim import AdamW
-from limn_amd.tensor import Tensor
+from limn_amd.seam import DType, Node, Op, Tensor, bfloat16, float32, int32, nn, optim
+
+Embedding, LayerNorm, Linear, parameters, AdamW = nn.Embedding, nn.LayerNorm, nn.Linear, nn.parameters, optim.AdamW
+
+GELU_C = math.sqrt(2.0 / math.pi)
+GELU_CUBIC = 0.044715
+GELU_EXP_LIMIT = 80.0  # exp(80) ~ 5.5e34: finite in float32 and bfloat16
+
+
+def gelu(x: Tensor) -> Tensor:
+    """GELU, tanh form: 0.5 x (1 + tanh(c (x + 0.044715 x^3))), c = sqrt(2/pi). Since
+    0.5 (1 + tanh(z)) = 1 / (1 + exp(-2z)), it is x / (1 + exp(-2c (x + 0.044715 x^3))): one
+    EXP and one RECIP, no tanh primitive. The exponent is capped at GELU_EXP_LIMIT: past it the
+    value (|x| e^-80 < 1e-33) is zero to float precision, and without the cap the exponential
+    overflows and the backward multiplies that infinity by zero."""
+    inner = ((x + GELU_CUBIC * (x * x * x)) * (-2.0 * GELU_C)).minimum(GELU_EXP_LIMIT)
+    return x * (inner.exp() + 1.0).reciprocal()
 
 
 @dataclass(frozen=True)

@@ -18,16 +18,16 @@ from __future__ import annotations
 
 import ctypes
 import math
+from typing import Any
 
 import numpy as np
 
-from limn_amd.codegen import LoopNest
 from limn_amd.dtypes import ABI_CODE
 from limn_amd.hip import runtime
 from limn_amd.hip.runtime import DEVICE_TO_DEVICE, DEVICE_TO_HOST, HOST_TO_DEVICE, check, check_limn
-from limn_amd.jit import Buffer, CompiledDevice, Runner
-from limn_amd.ops import FLOATS, Node, Op, accumulate_in
-from limn_amd.schedule import realized
+from limn_amd.seam import FLOATS, CompiledDevice, LoopNest, Node, Op, Runner, accumulate_in, realized
+
+Buffer = Any
 
 SDPA, SDPA_BWD_Q, SDPA_BWD_KV = "sdpa", "sdpa_bwd_q", "sdpa_bwd_kv"
 

@@ -37,9 +37,8 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from limn_amd.codegen import Index, Instr, LoopNest, Opcode, Valid
 from limn_amd.hip import runtime
-from limn_amd.ops import DType, Op, accumulate_in, bfloat16, float16, float32, float64, int8, int16, int32
+from limn_amd.seam import DType, Index, Instr, LoopNest, Op, Opcode, Valid, accumulate_in, bfloat16, float16, float32, float64, int8, int16, int32
 
 THREADS = 256
 
@@ -84,18 +83,18 @@ def literal(value: float | int, dtype: DType) -> str:
             return "(-2147483647 - 1)"
         return f"({VALUE_T[dtype]})({v})"
     v = float(value)
-    if dtype is float16:
+    if dtype == float16:
         v = float(np.float16(v))
-    elif dtype is bfloat16:
+    elif dtype == bfloat16:
         from limn_amd.dtypes import bf16_bits, bf16_values
 
         v = float(bf16_values(bf16_bits(np.array([v], dtype=np.float32)))[0])
     if math.isnan(v):
-        return "__builtin_nan(\"\")" if dtype is float64 else "__builtin_nanf(\"\")"
+        return "__builtin_nan(\"\")" if dtype == float64 else "__builtin_nanf(\"\")"
     if math.isinf(v):
         s = "-" if v < 0 else ""
-        return f"({s}__builtin_inf())" if dtype is float64 else f"({s}__builtin_inff())"
-    if dtype is float64:
+        return f"({s}__builtin_inf())" if dtype == float64 else f"({s}__builtin_inff())"
+    if dtype == float64:
         return repr(v)
     f = float(np.float32(v))
     if math.isinf(f):  # a finite double past float32's range
@@ -104,24 +103,24 @@ def literal(value: float | int, dtype: DType) -> str:
 
 
 def load_expr(dtype: DType, ref: str) -> str:
-    if dtype is bfloat16:
+    if dtype == bfloat16:
         return f"b2f({ref})"
-    if dtype is float16:
+    if dtype == float16:
         return f"h2f({ref})"
     return ref
 
 
 def store_expr(dtype: DType, value: str) -> str:
-    if dtype is bfloat16:
+    if dtype == bfloat16:
         return f"f2b({value})"
-    if dtype is float16:
+    if dtype == float16:
         return f"f2h({value})"
     return f"({STORE_T[dtype]})({value})"
 
 
 def arith(op: Op, srcs: tuple[str, ...], dtype: DType) -> str:
     t = VALUE_T[dtype]
-    wide = dtype is float64
+    wide = dtype == float64
     if op is Op.NEG:
         return f"({t})(-{srcs[0]})"
     if op is Op.EXP:
@@ -135,7 +134,7 @@ def arith(op: Op, srcs: tuple[str, ...], dtype: DType) -> str:
     if op is Op.ADD:
         return f"fadd(({t}){srcs[0]}, ({t}){srcs[1]})" if dtype in INTS else f"({srcs[0]} + {srcs[1]})"
     if op is Op.MUL:
-        if dtype is int32:
+        if dtype == int32:
             return f"(int)((unsigned){srcs[0]} * (unsigned){srcs[1]})"
         return f"({t})({srcs[0]} * {srcs[1]})"
     if op is Op.CMPLT:
@@ -207,9 +206,9 @@ def value_line(instr: Instr, bufs: Buffers) -> str:
     if op is Opcode.CAST:
         dt = instr.value_type
         src = instr.srcs[0]
-        if dt is bfloat16:
+        if dt == bfloat16:
             return f"const float {instr.dest} = b2f(f2b((float){src}));"
-        if dt is float16:
+        if dt == float16:
             return f"const float {instr.dest} = h2f(f2h((float){src}));"
         return f"const {t} {instr.dest} = ({t})({src});"
     if op is Opcode.GATHER:
@@ -545,7 +544,7 @@ def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned
     if write.opcode is Opcode.SCATTER:
         if out_dtype not in (float32, float64, int32):
             raise NotImplementedError(f"the hip device cannot scatter {out_dtype}; cast the table to float32 or int32")
-        if out_dtype is not int32:
+        if out_dtype != int32:
             return plan_scatter(nest, shape, bufs)
         lines.append(f"      atomicAdd(&{buf}[{render_index(index, True)}], ({STORE_T[out_dtype]}){write.srcs[0]});")
     elif store_run is not None:
@@ -1236,7 +1235,7 @@ def _stores_its_cells(nest: LoopNest) -> bool:
     target = nest.kernel.target.shape
     if tuple(nest.space) != tuple(target):
         return False
-    from limn_amd.codegen import contiguous_index
+    from limn_amd.seam import contiguous_index
 
     return shape.write.arg[1] == contiguous_index(tuple(target), [f"i{d}" for d in range(len(target))])
 

@@ -24,12 +24,12 @@ from dataclasses import dataclass
 from enum import Enum, auto
 from typing import TYPE_CHECKING, Any, NamedTuple
 
-from limn_amd.ops import FLOATS, INTS, DType, Node, Op
-from limn_amd.schedule import Kernel, addressed, realized, schedule
-from limn_amd.view import View, canonical_strides
+from .ops import FLOATS, INTS, DType, Node, Op
+from .schedule import Kernel, addressed, realized, schedule
+from .view import View, canonical_strides
 
 if TYPE_CHECKING:
-    from limn_amd.tensor import Tensor
+    from .tensor import Tensor
 
 ARITH_OPS = (Op.NEG, Op.EXP, Op.LOG, Op.SQRT, Op.RECIP, Op.ADD, Op.MUL, Op.CMPLT, Op.WHERE)
 

@@ -21,9 +21,9 @@ from collections.abc import Callable, Mapping
 from dataclasses import dataclass, replace
 from typing import Any
 
-from limn_amd.codegen import LoopNest, lower_all
-from limn_amd.ops import Custom, Node, Op, topological
-from limn_amd.schedule import realized, schedule
+from .codegen import LoopNest, lower_all
+from .ops import Custom, Node, Op, topological
+from .schedule import realized, schedule
 
 Buffer = Any
 Runner = Callable[[list[Buffer], list[Buffer]], None]

@@ -3,19 +3,14 @@
 Same classes, parameter layouts and initialisations as reference limn/nn.py (Linear stores
 (out, in) and draws uniform(+-1/sqrt(in)) like torch; LayerNorm starts at ones/zeros and uses the
 biased variance; Embedding draws N(0, 1) rows), so a model written against the reference builds
-the same graph here. `gelu` is the tanh approximation written in primitives, which the byte-level
-GPT of the C5 workload uses. Conv layers are not part of this build (its hot path has none).
+the same graph here. Conv layers are not part of this build (its hot path has none).
 """
 
 from __future__ import annotations
 
 import math
 
-from limn_amd.tensor import Tensor
-
-GELU_C = math.sqrt(2.0 / math.pi)
-GELU_CUBIC = 0.044715
-
+from .tensor import Tensor
 
 class Linear:
     """y = x @ weight^T + bias (reference limn/nn.py:16-26)."""
@@ -53,19 +48,6 @@ class Embedding:
 
     def __call__(self, indices: Tensor) -> Tensor:
         return self.weight.gather_rows(indices)
-
-
-GELU_EXP_LIMIT = 80.0  # exp(80) ~ 5.5e34: finite in float32 and bfloat16
-
-
-def gelu(x: Tensor) -> Tensor:
-    """GELU, tanh form: 0.5 x (1 + tanh(c (x + 0.044715 x^3))), c = sqrt(2/pi). Since
-    0.5 (1 + tanh(z)) = 1 / (1 + exp(-2z)), it is x / (1 + exp(-2c (x + 0.044715 x^3))): one
-    EXP and one RECIP, no tanh primitive. The exponent is capped at GELU_EXP_LIMIT: past it the
-    value (|x| e^-80 < 1e-33) is zero to float precision, and without the cap the exponential
-    overflows and the backward multiplies that infinity by zero."""
-    inner = ((x + GELU_CUBIC * (x * x * x)) * (-2.0 * GELU_C)).minimum(GELU_EXP_LIMIT)
-    return x * (inner.exp() + 1.0).reciprocal()
 
 
 def parameters(module: object) -> list[Tensor]:

@@ -15,7 +15,7 @@ from __future__ import annotations
 import math
 from dataclasses import dataclass
 
-from limn_amd.ops import Node, Op, topological
+from .ops import Node, Op, topological
 
 CUT_OPS = (Op.CONTIGUOUS, Op.ASSIGN, Op.SUM, Op.MAX, Op.GATHER, Op.SCATTER, Op.CUSTOM)
 _ADDRESSING = (Op.VIEW, Op.GATHER)

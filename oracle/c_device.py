@@ -24,14 +24,13 @@ import subprocess
 import tempfile
 import time
 from pathlib import Path
-from typing import Sequence
+from typing import Any, Sequence
 
 import numpy as np
 
-from limn_amd.codegen import Index, Instr, LoopNest, Opcode, Valid, loop_range
-from limn_amd.device import Buffer, HostDevice
-from limn_amd.jit import CompiledDevice, Runner
-from limn_amd.ops import DType, Op, float32, float64, int8, int16, int32
+from limn_amd.seam import CompiledDevice, DType, HostDevice, Index, Instr, LoopNest, Op, Opcode, Runner, Valid, float32, float64, int8, int16, int32, loop_range
+
+Buffer = Any
 
 C_TYPE = {float64: "double", float32: "float", int32: "int32_t", int16: "int16_t", int8: "int8_t"}
 
@@ -59,7 +58,7 @@ def literal(value: float | int, dtype: DType) -> str:
             return "NAN"
         if math.isinf(v):
             return "INFINITY" if v > 0 else "-INFINITY"
-        return repr(v) if dtype is float64 else f"{float(np.float32(v))!r}f"
+        return repr(v) if dtype == float64 else f"{float(np.float32(v))!r}f"
     bits = 8 * dtype.itemsize
     v = ((int(value) + (1 << (bits - 1))) % (1 << bits)) - (1 << (bits - 1))
     return "(-2147483647 - 1)" if v == -(1 << 31) else str(v)
@@ -67,7 +66,7 @@ def literal(value: float | int, dtype: DType) -> str:
 
 def _math(name: str, dtype: DType) -> str:
     # float64 uses C's double functions; everything else the float ones (an int operand converts)
-    return name if dtype is float64 else name + "f"
+    return name if dtype == float64 else name + "f"
 
 
 def arith(op: Op, srcs: Sequence[str], dtype: DType) -> str:

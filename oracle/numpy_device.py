@@ -23,10 +23,8 @@ import weakref
 
 import numpy as np
 
-from limn_amd.device import HostDevice
 from limn_amd.dtypes import STORAGE, bf16_bits
-from limn_amd.ops import DType, Node, Op, accumulate_in, bfloat16, float16, float32, float64, int8, int16, int32
-from limn_amd.view import View
+from limn_amd.seam import DType, HostDevice, Node, Op, accumulate_in, bfloat16, float16, float32, float64, int8, int16, int32, view
 from oracle import bf16
 from oracle import sdpa as attention
 
@@ -44,7 +42,7 @@ COMPUTE = {
 def cast(values: np.ndarray, dtype: DType) -> np.ndarray:
     """Values at `dtype`'s width: astype for numpy dtypes, round-to-nearest-even for bfloat16."""
     out = np.asarray(values)
-    if dtype is bfloat16:
+    if dtype == bfloat16:
         return bf16.rne(out.astype(np.float32))
     if out.dtype.kind == "f" and np.dtype(COMPUTE[dtype]).kind in "iu":
         with np.errstate(invalid="ignore"):
@@ -52,7 +50,7 @@ def cast(values: np.ndarray, dtype: DType) -> np.ndarray:
     return out.astype(COMPUTE[dtype], copy=False)
 
 
-def materialize(view: View, flat: np.ndarray) -> np.ndarray:
+def materialize(view: "view.View", flat: np.ndarray) -> np.ndarray:
     """Gather a view out of a flat array (reference limn/view.py:129-143): offset + sum(i*stride),
     masked positions read 0."""
     idx = np.full(view.shape, view.offset, dtype=np.int64)
@@ -70,11 +68,11 @@ def materialize(view: View, flat: np.ndarray) -> np.ndarray:
 
 def read_buffer(buf: np.ndarray, dtype: DType, shape) -> np.ndarray:
     raw = buf.view(STORAGE[dtype]).reshape(shape)
-    return bf16.widen(raw) if dtype is bfloat16 else raw
+    return bf16.widen(raw) if dtype == bfloat16 else raw
 
 
 def to_bytes(values: np.ndarray, dtype: DType) -> np.ndarray:
-    if dtype is bfloat16:
+    if dtype == bfloat16:
         return bf16_bits(np.asarray(values, dtype=np.float32)).view(np.uint8).reshape(-1)
     return np.ascontiguousarray(np.asarray(values).astype(STORAGE[dtype])).view(np.uint8).reshape(-1)
 
@@ -100,7 +98,7 @@ class NumpyDevice(HostDevice):
         return name in self.custom
 
     def execute(self, sinks: list[Node]) -> list:
-        from limn_amd.ops import topological
+        from limn_amd.seam import topological
 
         values = {node: self.compute(node) for node in topological(sinks)}
         assigns = [node for node in values if node.op is Op.ASSIGN]
@@ -129,7 +127,7 @@ class NumpyDevice(HostDevice):
         op = node.op
         with np.errstate(all="ignore"):
             if op is Op.CONST:
-                result = cast(np.full((), node.arg), node.dtype) if node.dtype is bfloat16 else np.full((), node.arg, dtype=COMPUTE[node.dtype])
+                result = cast(np.full((), node.arg), node.dtype) if node.dtype == bfloat16 else np.full((), node.arg, dtype=COMPUTE[node.dtype])
             elif op is Op.VIEW:
                 result = materialize(node.arg, srcs[0].reshape(-1))
             elif op is Op.NEG:

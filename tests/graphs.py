@@ -5,12 +5,12 @@ from __future__ import annotations
 
 import numpy as np
 
-from limn_amd import device as limn_device
+from limn_amd.seam import device as limn_device
 from limn_amd.dtypes import from_storage
-from limn_amd.ops import HALF_FLOATS
+from limn_amd.seam import HALF_FLOATS
 from oracle.numpy_device import NumpyDevice
 
-limn_device.register("numpy", NumpyDevice)
+limn_device.DEVICES["numpy"] = NumpyDevice
 
 GRAPHS = {
     "elementwise": lambda a, b: (a + b) * 2.0 - a,

@@ -10,10 +10,10 @@ import numpy as np
 import pytest
 
 from graphs import GRAPHS, check
-from limn_amd import device as limn_device
-from limn_amd.codegen import Opcode, lower_all
-from limn_amd.ops import Op, bfloat16, float16, float32, float64, int8, int16, int32, topological
-from limn_amd.tensor import Tensor, grad, scatter_rows
+from limn_amd.seam import device as limn_device
+from limn_amd.seam import Opcode, lower_all
+from limn_amd.seam import Op, bfloat16, float16, float32, float64, int8, int16, int32, topological
+from limn_amd.seam import Tensor, grad, scatter_rows
 from oracle import c_device
 from oracle import sdpa as ref
 

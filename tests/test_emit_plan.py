@@ -11,11 +11,11 @@ import math
 import numpy as np
 import pytest
 
-from limn_amd import device as limn_device
-from limn_amd.codegen import lower_all
-from limn_amd.ops import Op, bfloat16, float32, topological
-from limn_amd.schedule import realized, schedule
-from limn_amd.tensor import Tensor
+from limn_amd.seam import device as limn_device
+from limn_amd.seam import lower_all
+from limn_amd.seam import Op, bfloat16, float32, topological
+from limn_amd.seam import realized, schedule
+from limn_amd.seam import Tensor
 
 emit = pytest.importorskip("limn_amd.hip.emit")
 

@@ -10,12 +10,14 @@ import math
 import numpy as np
 import pytest
 
-from limn_amd import device as limn_device
-from limn_amd.capture import capture
+from limn_amd.seam import device as limn_device
+from limn_amd.seam import capture
 from limn_amd.gpt import GPT, GPTConfig, cross_entropy, make_trainer, synthetic_batch
-from limn_amd.nn import parameters
-from limn_amd.ops import bfloat16
-from limn_amd.tensor import grad, set_seed
+from limn_amd.seam import nn
+
+parameters = nn.parameters
+from limn_amd.seam import bfloat16
+from limn_amd.seam import grad, set_seed
 from oracle import sdpa as ref
 from oracle.numpy_device import NumpyDevice
 
@@ -58,7 +60,7 @@ def test_small_gpt_training_captured_equals_uncaptured(hipdev):
 
     plain_losses, plain_params, _ = run(False)
     cap_losses, cap_params, fn = run(True)
-    assert fn.wirings is not None
+    assert fn._feeds is not None
     assert cap_losses == plain_losses
     for a, b in zip(cap_params, plain_params):
         np.testing.assert_array_equal(a, b)

@@ -11,9 +11,9 @@ import numpy as np
 import pytest
 
 from graphs import GRAPHS, check
-from limn_amd import device as limn_device
-from limn_amd.ops import Op, bfloat16, float16, float32, float64, int8, int16, int32, topological
-from limn_amd.tensor import Tensor, grad
+from limn_amd.seam import device as limn_device
+from limn_amd.seam import Op, bfloat16, float16, float32, float64, int8, int16, int32, topological
+from limn_amd.seam import Tensor, grad
 
 pytestmark = pytest.mark.gpu
 
@@ -120,7 +120,7 @@ def test_scatter_with_repeats(hipdev):
     """512 values land on one row (reference tests/test_backend_cuda.py:125-131 allows 1e-4 for
     its atomics); here the total is np.add.at's, bit for bit. The values are drawn until adding
     them in reverse gives other bits, so that an unordered sum would fail."""
-    from limn_amd.tensor import scatter_rows
+    from limn_amd.seam import scatter_rows
 
     idx = np.zeros(512, dtype=np.int32)
     for seed in range(100):
@@ -144,7 +144,7 @@ def test_float_scatter_is_occurrence_ordered(hipdev, occurrences, rows, cols):
     """Float SCATTER equals np.add.at bit for bit (the oracle's rule, reference
     limn/device.py:153-158): each row adds its values in occurrence order onto 0. Negative
     indices count from the end as numpy's do; some rows get nothing and stay 0."""
-    from limn_amd.tensor import scatter_rows
+    from limn_amd.seam import scatter_rows
 
     values = order_sensitive(*occurrences, cols)
     idx = rng.integers(-rows, rows, size=occurrences).astype(np.int32)
@@ -154,7 +154,7 @@ def test_float_scatter_is_occurrence_ordered(hipdev, occurrences, rows, cols):
 def test_float64_scatter_and_computed_values_are_ordered(hipdev):
     """A float64 table, and values computed in the nest (a product then a sum, which must not be
     fused into one rounding)."""
-    from limn_amd.tensor import scatter_rows
+    from limn_amd.seam import scatter_rows
 
     idx = Tensor(rng.integers(0, 7, size=(400,)).astype(np.int32))
     v64 = Tensor(order_sensitive(400, 6).astype(np.float64) * 1.1, dtype=float64)
@@ -165,7 +165,7 @@ def test_float64_scatter_and_computed_values_are_ordered(hipdev):
 
 def test_scatter_grid_covers_more_rows_than_one_launch(hipdev):
     """A table of more (row, column block) items than the accumulating launch has workgroups."""
-    from limn_amd.tensor import scatter_rows
+    from limn_amd.seam import scatter_rows
 
     rows = (1 << 20) + 77
     idx = Tensor(rng.integers(0, rows, size=(5000,)).astype(np.int32))
@@ -206,7 +206,7 @@ def test_inlined_producer_read_through_a_pad_and_a_gather_index(hipdev):
 
 
 def test_scatter_int32_is_exact(hipdev):
-    from limn_amd.tensor import scatter_rows
+    from limn_amd.seam import scatter_rows
 
     values = Tensor(rng.integers(-1000, 1000, size=(300, 5)).astype(np.int32))
     idx = Tensor(rng.integers(0, 6, size=300).astype(np.int32))
@@ -214,7 +214,7 @@ def test_scatter_int32_is_exact(hipdev):
 
 
 def test_scatter_refuses_half_widths(hipdev):
-    from limn_amd.tensor import scatter_rows
+    from limn_amd.seam import scatter_rows
 
     values = Tensor(randf(8, 4), dtype=bfloat16)
     idx = Tensor(np.zeros(8, dtype=np.int32))
@@ -474,7 +474,7 @@ def test_config2_full_size(hipdev):
 
 def _plans(dev, t):
     """The emitter's plan for each nest of t's graph (which kernel family each nest got)."""
-    from limn_amd.codegen import lower_all
+    from limn_amd.seam import lower_all
     from limn_amd.hip.emit import plan_nest
 
     return [plan_nest(n) for n in lower_all([t.node])]

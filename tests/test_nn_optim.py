@@ -11,13 +11,18 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from limn_amd import device as limn_device
-from limn_amd.capture import capture
+from limn_amd.seam import device as limn_device
+from limn_amd.seam import capture
 from limn_amd.gpt import GPT, GPTConfig, cross_entropy, make_trainer, synthetic_batch
-from limn_amd.nn import Embedding, LayerNorm, Linear, gelu, parameters
-from limn_amd.ops import float32
-from limn_amd.optim import SGD, AdamW
-from limn_amd.tensor import Tensor, grad, set_seed
+from limn_amd.gpt import gelu
+from limn_amd.seam import nn
+
+Embedding, LayerNorm, Linear, parameters = nn.Embedding, nn.LayerNorm, nn.Linear, nn.parameters
+from limn_amd.seam import float32
+from limn_amd.seam import optim
+
+SGD, AdamW = optim.SGD, optim.AdamW
+from limn_amd.seam import Tensor, grad, set_seed
 from oracle import c_device
 from oracle.numpy_device import NumpyDevice
 
@@ -208,7 +213,7 @@ def _trained(captured: bool, steps: int = 5):
 def test_captured_training_is_bit_identical_to_running_the_step():
     plain_losses, plain_params, _ = _trained(False)
     cap_losses, cap_params, fn = _trained(True)
-    assert fn.wirings is not None  # replays really happened
+    assert fn._feeds is not None  # replays really happened
     assert cap_losses == plain_losses
     for a, b in zip(cap_params, plain_params):
         np.testing.assert_array_equal(a, b)

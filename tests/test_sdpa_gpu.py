@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 from conftest import DTYPES, download, storage_values, upload
-from limn_amd.ops import accumulate_in, custom
+from limn_amd.seam import accumulate_in, custom
 from oracle import sdpa as ref
 
 pytestmark = pytest.mark.gpu
