@@ -47,6 +47,13 @@ extern "C" __global__ void limn_commit_batch(const long long* __restrict__ table
 """
 
 
+def plan_context(order: list[Node], sinks: list[Node]) -> tuple[set, set]:
+    """(kept, custom_inputs) of one plan for the emitter: the nodes whose buffers must hold their
+    values (every sink, every CUSTOM src), and the CUSTOM srcs alone."""
+    custom_inputs = {realized(src) for n in order if n.op is Op.CUSTOM for src in n.srcs}
+    return {realized(s) for s in sinks} | custom_inputs, custom_inputs
+
+
 class HipBuffer:
     """Device bytes; the pointer returns to its device's pool when the last reference drops."""
 
@@ -201,8 +208,7 @@ class HipDevice(CompiledDevice):
         """The executor's plan_of, with the buffers that must hold their values recorded for
         runners(): the sinks and every CUSTOM src. runners() sees only the non-CUSTOM nests, and
         a contraction's epilogue may absorb a relu nest only when no one else reads the sum."""
-        self.plan_custom_inputs = {realized(src) for n in order if n.op is Op.CUSTOM for src in n.srcs}
-        self.plan_kept = {realized(s) for s in sinks} | self.plan_custom_inputs
+        self.plan_kept, self.plan_custom_inputs = plan_context(order, sinks)
         try:
             return super().plan_of(order, position, sinks)
         finally:

@@ -1363,14 +1363,44 @@ def merged_source(name: str, nests: list[LoopNest], plans: list[Planned], run: l
     return source, offset
 
 
-def nest_runners(dev, nests: list[LoopNest]):
-    """Compile every nest of a plan into one hipRTC program; one runner per nest, in order. A
-    contraction whose only reader is a relu nest runs as one MFMA launch with a relu epilogue,
-    from the relu nest's runner (see epilogue_pairs); small broadcast producers run inside their
-    readers (inline_producers); groups of small independent elementwise nests share one launch
-    from their last member's runner (merge_runs)."""
+@dataclass
+class Program:
+    """A plan's nests as the device will run them (see nest_runners): each nest's Planned, the
+    relu epilogues `pairs` {contraction: relu nest}, the inlined producers, the merged runs
+    {last member: (members, launch)}, and the hipRTC source and kernel names of the whole plan."""
+
+    plans: list[Planned]
+    pairs: dict[int, int]
+    inlined: "InlineSet"
+    merged: dict[int, tuple[list[int], Launch]]
+    source: str
+    names: list[str]
+
+    def role(self, k: int) -> str:
+        """What nest k's runner does: 'stash' (a contraction whose relu nest launches it),
+        'epilogue', 'inlined', 'deferred' (a merged run's earlier member), 'merged' (the run's
+        launch), 'contraction' or 'launch'."""
+        if k in self.pairs:
+            return "stash"
+        if k in self.inlined.producers:
+            return "inlined"
+        if k in self.merged:
+            return "merged"
+        if any(k in run for run, _ in self.merged.values()):
+            return "deferred"
+        if k in set(self.pairs.values()):
+            return "epilogue"
+        return "contraction" if self.plans[k].contraction is not None else "launch"
+
+
+def plan_program(nests: list[LoopNest], kept: set | None, custom_inputs: set | None) -> Program:
+    """Plan every nest of one executor plan: contractions and their relu epilogues
+    (epilogue_pairs), small broadcast producers evaluated in their readers (inline_producers),
+    groups of small independent nests sharing a launch (merge_runs). `kept` is the buffers the
+    plan must keep (sinks and CUSTOM inputs) and `custom_inputs` the CUSTOM inputs alone, both
+    recorded by the device's plan_of; None for either turns the optimisations that need it off.
+    Touches no GPU."""
     plans = [plan_nest(n) for n in nests]
-    kept = getattr(dev, "plan_kept", None)
     pairs = epilogue_pairs(nests, plans, kept)
     fused = {j: i for i, j in pairs.items()}
     for j in fused:
@@ -1381,8 +1411,8 @@ def nest_runners(dev, nests: list[LoopNest]):
             plans[c] = plan_nest(nest, inlined)
     for j in inlined.producers:
         plans[j] = Planned("", [], notes={"inlined": True})
-    runs = merge_runs(nests, plans, getattr(dev, "plan_custom_inputs", None), inlined, pairs)
-    merged: dict[int, tuple[list[int], Launch]] = {}  # a run's last member -> (run, its launch)
+    runs = merge_runs(nests, plans, custom_inputs, inlined, pairs)
+    merged: dict[int, tuple[list[int], Launch]] = {}
     merged_sources = []
     for run in runs:
         name = f"{nests[run[0]].name}_to_{nests[run[-1]].name}"
@@ -1393,40 +1423,49 @@ def nest_runners(dev, nests: list[LoopNest]):
     names = [launch.name for k, p in enumerate(plans) if k not in in_run for launch in p.launches]
     names += [launch.name for _, launch in merged.values()]
     kept_sources = [p.source for k, p in enumerate(plans) if k not in in_run]
-    functions = runtime.load_functions(PRELUDE + "\n".join(kept_sources + merged_sources), names) if names else {}
+    source = PRELUDE + "\n".join(kept_sources + merged_sources) if names else ""
+    return Program(plans, pairs, inlined, merged, source, names)
+
+
+def nest_runners(dev, nests: list[LoopNest]):
+    """Compile every nest of a plan into one hipRTC program; one runner per nest, in order. A
+    contraction whose only reader is a relu nest runs as one MFMA launch with a relu epilogue,
+    from the relu nest's runner (see epilogue_pairs); small broadcast producers run inside their
+    readers (inline_producers); groups of small independent elementwise nests share one launch
+    from their last member's runner (merge_runs)."""
+    prog = plan_program(nests, getattr(dev, "plan_kept", None), getattr(dev, "plan_custom_inputs", None))
+    plans, pairs, inlined, merged = prog.plans, prog.pairs, prog.inlined, prog.merged
+    functions = runtime.load_functions(prog.source, prog.names) if prog.names else {}
     runners = []
     operands: dict[int, list] = {}  # a fused contraction's inputs, from its call to its relu's
     producer_inputs: dict[int, list] = {}  # an inlined producer's inputs, from its call to its readers'
     deferred: dict[int, tuple] = {}  # a merged run member's (inputs, outs), from its call to the run's launch
     for k, (nest, plan) in enumerate(zip(nests, plans)):
-        if k in pairs:
+        role = prog.role(k)
+        if role == "stash":
             runners.append(_stash_runner(operands, k))
-            continue
-        if k in inlined.producers:
+        elif role == "inlined":
             runners.append(_keep_runner(producer_inputs, k))
-            continue
-        if k in merged:
+        elif role == "merged":
             run, launch = merged[k]
             count = sum(len(plans[c].notes["params"]) for c in run)
             runners.append(_merged_runner(_launcher(dev, functions[launch.name], launch, count - 1), run, nests, inlined,
                                           producer_inputs, deferred, k))
-            continue
-        if k in in_run:
+        elif role == "deferred":
             runners.append(_defer_runner(deferred, k))
-            continue
-        if k in fused:
-            runners.append(_epilogue_runner(dev, plans[fused[k]].contraction, operands, fused[k]))
-            continue
-        if plan.contraction is not None:
+        elif role == "epilogue":
+            source = next(i for i, j in pairs.items() if j == k)
+            runners.append(_epilogue_runner(dev, plans[source].contraction, operands, source))
+        elif role == "contraction":
             runners.append(_contraction_runner(dev, plan.contraction))
-            continue
-        extras = inlined.extras(nest)
-        nin = len(nest.kernel.inputs) + len(extras)
-        launchers = []
-        for launch in plan.launches:
-            count = {"io": nin + 1, "io_scratch": nin + 1, "io_scratch_out": nin + 2}.get(launch.args, 2)
-            launchers.append((launch.args, _launcher(dev, functions[launch.name], launch, count - 1)))
-        runners.append(_make_runner(dev, launchers, plan.scratch_bytes, extras, producer_inputs))
+        else:
+            extras = inlined.extras(nest)
+            nin = len(nest.kernel.inputs) + len(extras)
+            launchers = []
+            for launch in plan.launches:
+                count = {"io": nin + 1, "io_scratch": nin + 1, "io_scratch_out": nin + 2}.get(launch.args, 2)
+                launchers.append((launch.args, _launcher(dev, functions[launch.name], launch, count - 1)))
+            runners.append(_make_runner(dev, launchers, plan.scratch_bytes, extras, producer_inputs))
     return runners
 
 

@@ -17,9 +17,9 @@ ROOT = Path(__file__).resolve().parent.parent
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
+from limn_amd.seam import bfloat16, float16, float32, float64, Node, Op  # noqa: E402
 from limn_amd.seam import device as limn_device  # noqa: E402
 from limn_amd.dtypes import STORAGE, from_storage, to_storage  # noqa: E402
-from limn_amd.seam import Node, Op, bfloat16, float16, float32, float64  # noqa: E402
 from oracle.numpy_device import NumpyDevice  # noqa: E402
 
 limn_device.DEVICES["numpy"] = NumpyDevice  # the oracle, as a selectable device for every test

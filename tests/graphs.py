@@ -5,9 +5,9 @@ from __future__ import annotations
 
 import numpy as np
 
+from limn_amd.seam import HALF_FLOATS
 from limn_amd.seam import device as limn_device
 from limn_amd.dtypes import from_storage
-from limn_amd.seam import HALF_FLOATS
 from oracle.numpy_device import NumpyDevice
 
 limn_device.DEVICES["numpy"] = NumpyDevice

@@ -10,10 +10,8 @@ import numpy as np
 import pytest
 
 from graphs import GRAPHS, check
+from limn_amd.seam import bfloat16, float16, float32, float64, grad, int16, int32, int8, lower_all, Op, Opcode, scatter_rows, Tensor, topological
 from limn_amd.seam import device as limn_device
-from limn_amd.seam import Opcode, lower_all
-from limn_amd.seam import Op, bfloat16, float16, float32, float64, int8, int16, int32, topological
-from limn_amd.seam import Tensor, grad, scatter_rows
 from oracle import c_device
 from oracle import sdpa as ref
 

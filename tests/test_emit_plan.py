@@ -11,11 +11,8 @@ import math
 import numpy as np
 import pytest
 
+from limn_amd.seam import bfloat16, float32, lower_all, Op, realized, schedule, Tensor, topological
 from limn_amd.seam import device as limn_device
-from limn_amd.seam import lower_all
-from limn_amd.seam import Op, bfloat16, float32, topological
-from limn_amd.seam import realized, schedule
-from limn_amd.seam import Tensor
 
 emit = pytest.importorskip("limn_amd.hip.emit")
 

@@ -10,16 +10,13 @@ import math
 import numpy as np
 import pytest
 
+from limn_amd.seam import bfloat16, capture, grad, nn, set_seed
 from limn_amd.seam import device as limn_device
-from limn_amd.seam import capture
 from limn_amd.gpt import GPT, GPTConfig, cross_entropy, make_trainer, synthetic_batch
-from limn_amd.seam import nn
-
-parameters = nn.parameters
-from limn_amd.seam import bfloat16
-from limn_amd.seam import grad, set_seed
 from oracle import sdpa as ref
 from oracle.numpy_device import NumpyDevice
+
+parameters = nn.parameters
 
 pytestmark = pytest.mark.gpu
 

@@ -11,9 +11,8 @@ import numpy as np
 import pytest
 
 from graphs import GRAPHS, check
+from limn_amd.seam import bfloat16, float16, float32, float64, grad, int16, int32, int8, Op, Tensor, topological
 from limn_amd.seam import device as limn_device
-from limn_amd.seam import Op, bfloat16, float16, float32, float64, int8, int16, int32, topological
-from limn_amd.seam import Tensor, grad
 
 pytestmark = pytest.mark.gpu
 

@@ -11,20 +11,14 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from limn_amd.seam import capture, float32, grad, nn, optim, set_seed, Tensor
 from limn_amd.seam import device as limn_device
-from limn_amd.seam import capture
-from limn_amd.gpt import GPT, GPTConfig, cross_entropy, make_trainer, synthetic_batch
-from limn_amd.gpt import gelu
-from limn_amd.seam import nn
-
-Embedding, LayerNorm, Linear, parameters = nn.Embedding, nn.LayerNorm, nn.Linear, nn.parameters
-from limn_amd.seam import float32
-from limn_amd.seam import optim
-
-SGD, AdamW = optim.SGD, optim.AdamW
-from limn_amd.seam import Tensor, grad, set_seed
+from limn_amd.gpt import GPT, GPTConfig, cross_entropy, gelu, make_trainer, synthetic_batch
 from oracle import c_device
 from oracle.numpy_device import NumpyDevice
+
+Embedding, LayerNorm, Linear, parameters = nn.Embedding, nn.LayerNorm, nn.Linear, nn.parameters
+SGD, AdamW = optim.SGD, optim.AdamW
 
 rng = np.random.default_rng(5)
 
