@@ -169,10 +169,14 @@ class HipDevice(CompiledDevice):
     COMMIT_CHUNK = 1 << 16  # bytes per workgroup of the commit kernel
 
     def _flush_commits(self) -> None:
+        """Launch the queued commits as one kernel over a (value, target, bytes) table. The queue is
+        taken first, so an allocation failure below (whose trim() finishes the batch) finds
+        nothing left to flush; a grown table is allocated before the old one is released."""
         if not self._commits:
             return
+        commits, self._commits, self._commit_targets = self._commits, [], set()
         entries = []
-        for target, value in self._commits:
+        for target, value in commits:
             for off in range(0, value.nbytes, self.COMMIT_CHUNK):
                 entries.append((value.ptr + off, target.ptr + off, min(self.COMMIT_CHUNK, value.nbytes - off)))
         if self._committed:
@@ -181,13 +185,14 @@ class HipDevice(CompiledDevice):
         table = np.array(entries, dtype=np.int64)
         host, cap, dev_table = self._commit_table or (0, 0, None)
         if cap < len(entries):
+            cap = max(len(entries), 2 * cap, 1024)
+            grown = self._alloc(cap * 24)
+            ptr = ctypes.c_void_p()
+            check(self.api.hipHostMalloc(ctypes.byref(ptr), cap * 24, 0), "allocating a pinned commit table")
             if host:
                 check(self.api.hipStreamSynchronize(None), "waiting for a commit table")
                 self.api.hipHostFree(ctypes.c_void_p(host))
-            cap = max(len(entries), 2 * cap, 1024)
-            ptr = ctypes.c_void_p()
-            check(self.api.hipHostMalloc(ctypes.byref(ptr), cap * 24, 0), "allocating a pinned commit table")
-            host, dev_table = ptr.value, self._alloc(cap * 24)
+            host, dev_table = ptr.value, grown
             self._commit_table = (host, cap, dev_table)
         ctypes.memmove(host, table.ctypes.data, table.nbytes)
         check(self.api.hipMemcpyAsync(ctypes.c_void_p(dev_table.ptr), ctypes.c_void_p(host), table.nbytes, HOST_TO_DEVICE, None), "uploading a commit table")
@@ -195,9 +200,7 @@ class HipDevice(CompiledDevice):
         args = (ctypes.c_void_p * 2)(ctypes.c_void_p(dev_table.ptr), ctypes.c_void_p(len(entries)))
         params = (ctypes.c_void_p * 2)(*[ctypes.addressof(args) + k * ctypes.sizeof(ctypes.c_void_p) for k in range(2)])
         check(self.api.hipModuleLaunchKernel(fn, len(entries), 1, 1, 256, 1, 1, 0, None, params, None), "launching the commits")
-        self._committed += self._commits
-        self._commits = []
-        self._commit_targets = set()
+        self._committed += commits
 
     def finish(self) -> None:
         self._flush_commits()

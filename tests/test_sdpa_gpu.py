@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 from conftest import DTYPES, download, storage_values, upload
-from limn_amd.seam import accumulate_in, custom
+from limn_amd.seam import accumulate_in, bfloat16, custom, float32
 from oracle import sdpa as ref
 
 pytestmark = pytest.mark.gpu
@@ -188,32 +188,62 @@ def test_config1_matches_torch_golden(hipdev):
         np.testing.assert_allclose(float((val.astype(np.float64) ** 2).sum()), float(g[f"{key}_sumsq"]), rtol=1e-4)
 
 
-def test_config4_full_size_two_heads(hipdev):
-    """BASELINE config 4 at its full shape (bf16, causal, B=8 H=16 S=4096 D=128, seed 4):
-    the GPU runs all 128 heads; heads are independent, so two of them (the first and the last)
-    are diffed against the oracle, and every output must be finite."""
+def _poisoned_pool(dev, sizes) -> None:
+    """Return buffers of these sizes to the device's pool filled with 0xFF bytes (NaN in bf16 and
+    f32): the next outputs of those sizes start as NaN, so a cell a kernel never writes fails
+    the finiteness check instead of passing on stale finite bytes."""
+    held = [dev._alloc(n) for n in sizes]
+    for buf in held:
+        dev.copyin(buf, np.full(buf.nbytes, 0xFF, dtype=np.uint8))
+    del held
+
+
+# One head from each of the eight runs head_and_block gives the XCDs (16 consecutive heads each
+# at C4), plus the last head; flat index b * H + h.
+C4_HEADS = (0, 21, 42, 63, 68, 89, 110, 127)
+
+
+def test_config4_full_size_every_xcd(hipdev):
+    """BASELINE config 4 at its full shape (bf16, causal, B=8 H=16 S=4096 D=128, seed 4).
+
+    Every output starts as NaN bytes and must come back finite (all 128 heads, forward and
+    backward). The kernels number workgroups head-major per XCD (each XCD a run of 16 heads), so
+    one head of every run is diffed against the oracle, forward and backward."""
+    from limn_amd.dtypes import bf16_bits, bf16_values
+
     B, H, S, D = 8, 16, 4096, 128
     rng = np.random.default_rng(4)
-    from limn_amd.dtypes import bf16_bits, bf16_values
 
     def rnd():
         return bf16_values(bf16_bits(rng.standard_normal((B, H, S, D), dtype=np.float32)))
 
     q, k, v, do = rnd(), rnd(), rnd(), rnd()
-    out, lse = forward(hipdev, q, k, v, None, True, "bfloat16")
+    scale = D**-0.5
+    big, stat = B * H * S * D * 2, B * H * S * 4
+    q_n, k_n, v_n, do_n = (upload(hipdev, x, bfloat16) for x in (q, k, v, do))
+    print("C4 forward, NaN-poisoned outputs", flush=True)
+    _poisoned_pool(hipdev, [big, stat])
+    o_node, l_node = custom("sdpa", (q_n, k_n, v_n), (True, scale), ((bfloat16, q.shape), (float32, (B, H, S, 1))))
+    bo, bl = hipdev.execute([o_node, l_node])
+    out, lse = download(hipdev, bo, bfloat16, q.shape), download(hipdev, bl, float32, (B, H, S, 1))
     assert np.isfinite(out).all() and np.isfinite(lse).all()
     delta = (do * out).sum(axis=-1, keepdims=True).astype(np.float32)
-    dq, dk, dv = backward(hipdev, q, k, v, do, lse, delta, None, True, "bfloat16")
+    srcs = (q_n, k_n, v_n, do_n, upload(hipdev, lse, float32), upload(hipdev, delta, float32))
+    print("C4 backward, NaN-poisoned outputs", flush=True)
+    _poisoned_pool(hipdev, [big, big, big])
+    (dq_n,) = custom("sdpa_bwd_q", srcs, (True, scale), ((bfloat16, q.shape),))
+    dk_n, dv_n = custom("sdpa_bwd_kv", srcs, (True, scale), ((bfloat16, q.shape), (bfloat16, q.shape)))
+    dq, dk, dv = (download(hipdev, b, bfloat16, q.shape) for b in hipdev.execute([dq_n, dk_n, dv_n]))
     for g in (dq, dk, dv):
         assert np.isfinite(g).all()
-    scale = D**-0.5
-    for b, h in ((0, 0), (B - 1, H - 1)):
+    for flat in C4_HEADS:
+        b, h = divmod(flat, H)
         args = [x[b, h] for x in (q, k, v)]
         want_out, want_lse = ref.sdpa(*args, causal=True, scale=scale, dtype="bfloat16", block_size=256)
-        np.testing.assert_allclose(out[b, h], want_out, rtol=1e-2, atol=1e-2)
-        np.testing.assert_allclose(lse[b, h], want_lse, rtol=1e-2, atol=1e-2)
+        np.testing.assert_allclose(out[b, h], want_out, rtol=1e-2, atol=1e-2, err_msg=f"O head {flat}")
+        np.testing.assert_allclose(lse[b, h], want_lse, rtol=1e-2, atol=1e-2, err_msg=f"L head {flat}")
         bargs = (*args, do[b, h], lse[b, h], delta[b, h])
         want_dq = ref.sdpa_backward_q(*bargs, causal=True, scale=scale, dtype="bfloat16", block_size=256)
         want_dk, want_dv = ref.sdpa_backward_kv(*bargs, causal=True, scale=scale, dtype="bfloat16", block_size=256)
-        for got, want in ((dq[b, h], want_dq), (dk[b, h], want_dk), (dv[b, h], want_dv)):
-            np.testing.assert_allclose(got, want, rtol=3e-2, atol=3e-2)
+        for name, got, want in (("dQ", dq[b, h], want_dq), ("dK", dk[b, h], want_dk), ("dV", dv[b, h], want_dv)):
+            np.testing.assert_allclose(got, want, rtol=3e-2, atol=3e-2, err_msg=f"{name} head {flat}")
