@@ -109,6 +109,21 @@ int limn_hip_matmul(const void* a, const void* b, void* c, int dtype, int64_t ba
  * counterpart in the reference (its contraction kernel never splits). */
 int64_t limn_hip_matmul_workspace(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K);
 
+/*
+ * limn_hip_matmul without a caller workspace and without allocating: the split-k slices (see
+ * above) go to a static device array of LIMN_HIP_SCRATCH_BYTES, one per GPU, held until the process
+ * ends. For callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc); no counterpart in the reference. Results equal
+ * limn_hip_matmul's with a large enough workspace, bit for bit. Refuses (LIMN_HIP_EINVAL) a
+ * contraction whose slices need more than LIMN_HIP_SCRATCH_BYTES (limn_hip_matmul_workspace says
+ * how much). Every call on one GPU shares that GPU's array: calls that overlap on one GPU (on two
+ * streams, or from two threads) race on it and must be ordered by the caller.
+ */
+#define LIMN_HIP_SCRATCH_BYTES (128ll << 20)
+int limn_hip_matmul_noalloc(const void* a, const void* b, void* c, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+                            int64_t a_batch, int64_t a_m, int64_t a_k, int64_t b_batch, int64_t b_k, int64_t b_n,
+                            int64_t c_batch, int64_t c_m, int64_t c_n, int epilogue, void* stream);
+
 /* 1 when limn_hip_matmul has a kernel for this dtype and operand layout, else 0 (the device
  * then keeps the contraction on the general reduce kernels). */
 int limn_hip_matmul_supported(int dtype, int64_t M, int64_t N, int64_t K, int64_t a_batch, int64_t a_m, int64_t a_k,

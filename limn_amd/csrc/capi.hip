@@ -4,6 +4,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "matmul.h"
 #include "sdpa.h"
 
@@ -72,6 +74,51 @@ static int run(SdpaPass pass, const SdpaArgs& a) {
               (long long)a.hd, (long long)a.hd_v);
 }
 
+// The argument rules both matmul entry points apply before launching anything.
+static int check_matmul(const char* name, const void* a, const void* b, const void* c, int dtype, const MatmulShape& s,
+                        int epilogue) {
+  if (dtype != LIMN_HIP_BFLOAT16 && dtype != LIMN_HIP_FLOAT16)
+    return fail(LIMN_HIP_EUNSUPPORTED, "%s: the MFMA contraction takes bfloat16 or float16, not dtype code %d", name, dtype);
+  if (s.batch < 1 || s.M < 1 || s.N < 1 || s.K < 1)
+    return fail(LIMN_HIP_EINVAL, "%s: sizes must be positive (batch %lld, M %lld, N %lld, K %lld)", name,
+                (long long)s.batch, (long long)s.M, (long long)s.N, (long long)s.K);
+  if (a == nullptr || b == nullptr || c == nullptr) return fail(LIMN_HIP_EINVAL, "%s: null buffer", name);
+  if (epilogue != MATMUL_EPILOGUE_NONE && epilogue != MATMUL_EPILOGUE_RELU)
+    return fail(LIMN_HIP_EINVAL, "%s: unknown epilogue %d", name, epilogue);
+  if (!matmul_layout_ok(s))
+    return fail(LIMN_HIP_EUNSUPPORTED, "%s: operands must be contiguous along m/n or k with 16-byte aligned rows", name);
+  if (((uintptr_t)a | (uintptr_t)b) % 16 != 0) return fail(LIMN_HIP_EUNSUPPORTED, "%s: operands must be 16-byte aligned", name);
+  return LIMN_HIP_OK;
+}
+
+// The split-k scratch of limn_hip_matmul_noalloc: a static device array, one copy per GPU, held
+// until the process ends. In host code `scratch` names a host-side stand-in, not device memory:
+// its device address is looked up once per device (hipGetSymbolAddress, that device current)
+// and only that address is handed to kernels.
+__device__ __align__(256) unsigned char scratch[LIMN_HIP_SCRATCH_BYTES];
+
+constexpr int SCRATCH_DEVICES = 64;
+static void* scratch_at[SCRATCH_DEVICES];
+static std::mutex scratch_lock;
+
+static int scratch_address(void** out) {
+  int device = -1;
+  int rc = check_hip(hipGetDevice(&device), "reading the current device");
+  if (rc != LIMN_HIP_OK) return rc;
+  if (device < 0 || device >= SCRATCH_DEVICES)
+    return fail(LIMN_HIP_EUNSUPPORTED, "matmul_noalloc: device %d is past the %d devices the scratch table holds", device,
+                SCRATCH_DEVICES);
+  std::lock_guard<std::mutex> hold(scratch_lock);
+  if (scratch_at[device] == nullptr) {
+    void* found = nullptr;
+    rc = check_hip(hipGetSymbolAddress(&found, HIP_SYMBOL(scratch)), "finding the static matmul scratch");
+    if (rc != LIMN_HIP_OK) return rc;
+    scratch_at[device] = found;
+  }
+  *out = scratch_at[device];
+  return LIMN_HIP_OK;
+}
+
 }  // namespace limn
 
 using namespace limn;
@@ -127,19 +174,27 @@ int limn_hip_matmul(const void* a, const void* b, void* c, int dtype, int64_t ba
                     int64_t a_batch, int64_t a_m, int64_t a_k, int64_t b_batch, int64_t b_k, int64_t b_n, int64_t c_batch,
                     int64_t c_m, int64_t c_n, int epilogue, void* workspace, int64_t workspace_bytes, void* stream) {
   MatmulShape s = {batch, M, N, K, a_batch, a_m, a_k, b_batch, b_k, b_n, c_batch, c_m, c_n};
-  if (dtype != LIMN_HIP_BFLOAT16 && dtype != LIMN_HIP_FLOAT16)
-    return fail(LIMN_HIP_EUNSUPPORTED, "matmul: the MFMA contraction takes bfloat16 or float16, not dtype code %d", dtype);
-  if (batch < 1 || M < 1 || N < 1 || K < 1)
-    return fail(LIMN_HIP_EINVAL, "matmul: sizes must be positive (batch %lld, M %lld, N %lld, K %lld)", (long long)batch,
-                (long long)M, (long long)N, (long long)K);
-  if (a == nullptr || b == nullptr || c == nullptr) return fail(LIMN_HIP_EINVAL, "matmul: null buffer");
-  if (epilogue != MATMUL_EPILOGUE_NONE && epilogue != MATMUL_EPILOGUE_RELU)
-    return fail(LIMN_HIP_EINVAL, "matmul: unknown epilogue %d", epilogue);
-  if (!matmul_layout_ok(s))
-    return fail(LIMN_HIP_EUNSUPPORTED, "matmul: operands must be contiguous along m/n or k with 16-byte aligned rows");
-  if (((uintptr_t)a | (uintptr_t)b) % 16 != 0) return fail(LIMN_HIP_EUNSUPPORTED, "matmul: operands must be 16-byte aligned");
+  const int rc = check_matmul("matmul", a, b, c, dtype, s, epilogue);
+  if (rc != LIMN_HIP_OK) return rc;
   if (workspace_bytes < 0) return fail(LIMN_HIP_EINVAL, "matmul: negative workspace size");
   return launch_matmul(a, b, c, dtype, s, epilogue, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int limn_hip_matmul_noalloc(const void* a, const void* b, void* c, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+                            int64_t a_batch, int64_t a_m, int64_t a_k, int64_t b_batch, int64_t b_k, int64_t b_n,
+                            int64_t c_batch, int64_t c_m, int64_t c_n, int epilogue, void* stream) {
+  MatmulShape s = {batch, M, N, K, a_batch, a_m, a_k, b_batch, b_k, b_n, c_batch, c_m, c_n};
+  int rc = check_matmul("matmul_noalloc", a, b, c, dtype, s, epilogue);
+  if (rc != LIMN_HIP_OK) return rc;
+  const int64_t need = matmul_workspace_bytes(s);
+  if (need > (int64_t)LIMN_HIP_SCRATCH_BYTES)
+    return fail(LIMN_HIP_EINVAL,
+                "matmul_noalloc: this contraction splits k into slices that need %lld bytes of scratch, more than the "
+                "%lld-byte static scratch; call limn_hip_matmul with a workspace instead",
+                (long long)need, (long long)LIMN_HIP_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0 && (rc = scratch_address(&ws)) != LIMN_HIP_OK) return rc;
+  return launch_matmul(a, b, c, dtype, s, epilogue, ws, need, (hipStream_t)stream);
 }
 
 int64_t limn_hip_matmul_workspace(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K) {

@@ -88,3 +88,20 @@ def test_null_buffers_are_refused():
     lib = runtime.kernels()
     rc = lib.limn_hip_sdpa_bwd_q(FAKE, FAKE, FAKE, None, FAKE, FAKE, None, FAKE, 1, 1, 4, 4, 8, 8, 0, 0.5, None)
     assert rc == 1 and "null" in lib.limn_hip_last_error().decode()
+
+
+def test_every_split_fits_the_static_scratch():
+    """limn_hip_matmul_noalloc keeps split-k slices in a static array of LIMN_HIP_SCRATCH_BYTES.
+    The planner splits only while output tiles x slices stay under two waves of 256 workgroups,
+    so no contraction needs more; swept over batch, M, N (multiples of 64) and k."""
+    lib = runtime.kernels()
+    text = HEADER.read_text()
+    limit = int(re.search(r"#define LIMN_HIP_SCRATCH_BYTES \((\d+)ll << (\d+)\)", text).group(1)) << 20
+    assert limit == 128 << 20
+    worst = 0
+    for batch in (1, 2, 3, 8):
+        for m in range(64, 4097, 192):
+            for n in range(64, 4097, 320):
+                for k in (1024, 5376, 1 << 14, 1 << 20):
+                    worst = max(worst, lib.limn_hip_matmul_workspace(3, batch, m, n, k))
+    assert 0 < worst <= limit
