@@ -3,10 +3,11 @@
 Default workload (the north star's headline target): causal flash
 attention, bf16, B=8 H=16 S=4096 D=128, scale 1/sqrt(128), inputs N(0,1) from
 np.random.default_rng(4) drawn in the order q, k, v, dO. One step is one forward and one
-backward over the batch: the three CUSTOM kernels sdpa, sdpa_bwd_q and sdpa_bwd_kv, launched
-back to back on the null stream through the device's runners (the same callables its plans
-call). delta = rowsum(dO * O) is an ordinary reduce in limn's graph; it is computed once before
-timing and reported apart, as the north star's target is for the three CUSTOM kernels.
+backward over the batch: CUSTOM sdpa, the delta row-sum rowsum(dO * O) (an ordinary SUM nest of
+limn's graph, emitted by the device), then CUSTOM sdpa_bwd_q and sdpa_bwd_kv, launched back to
+back on the null stream through the device's runners (the same callables its plans call). The
+step's value includes the delta nest; `custom_kernels` reports the three CUSTOM kernels alone
+(the north star's target) and `delta_kernel` the nest's HBM rate.
 
 Work is counted the FlashAttention way (causal = half the square): one causal matmul is
 U = 2*B*H*S*S*D/2; the forward is 2U (QK^T, PV), the backward 5U (S, dP, dV, dK, dQ), so a step
@@ -16,6 +17,10 @@ dK), sdpa_bwd_q 1U (dQ; its recomputed S and dP are executed, not algorithmic).
 Timing: W untimed warmup steps, then K steps between two hipEvents on the null stream with a
 device synchronize on both sides; per-kernel averages come from events recorded between the
 launches of every timed step.
+
+roofline.traffic is the dominant kernel's HBM bytes per launch from profiles/hbm_traffic.json
+(rocprofv3 FETCH_SIZE/WRITE_SIZE passes reduced by `bench.py --summarize`); it is null when
+those passes were taken on other kernel sources than this build's (`traffic_source` says which).
 
 CPU baseline (`cpu_baseline`): oracle/c_device.py, limn's single-threaded C backend restated
 over this package's loop-nest IR (reference limn/backend_c.py), timed inside its compiled nests
@@ -39,19 +44,57 @@ import numpy as np
 
 MFMA_BF16_PEAK = 2.5e15  # dense bf16 MFMA flop/s, MI355X published
 HBM_PEAK = 8.0e12  # bytes/s
-TRAFFIC = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+ROOT = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+# the sources whose compiled kernels the traffic figures describe
+KERNEL_SOURCES = ("limn_amd/csrc/*.hip", "limn_amd/csrc/*.h", "include/*.h", "limn_amd/hip/emit.py")
+
+
+def build_stamp() -> str:
+    """A short hash of every kernel source (hand-written and emitter): what a profile's counter
+    figures are valid for."""
+    import glob
+    import hashlib
+
+    digest = hashlib.sha256()
+    for pattern in KERNEL_SOURCES:
+        for path in sorted(glob.glob(os.path.join(ROOT, pattern))):
+            digest.update(os.path.relpath(path, ROOT).encode())
+            with open(path, "rb") as f:
+                digest.update(f.read())
+    return digest.hexdigest()[:12]
+
+
+def _traffic_table() -> dict:
+    try:
+        with open(TRAFFIC) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
 
 
 def traffic(key: str):
     """HBM bytes per launch of one kernel (read + written), from the rocprofv3 FETCH_SIZE and
-    WRITE_SIZE passes recorded in profiles/hbm_traffic.json, each counter scaled by what it reads
-    for a plain copy of known size. None when that kernel has no recorded pass."""
-    try:
-        with open(TRAFFIC) as f:
-            entry = json.load(f)["kernels"].get(key)
-    except (OSError, ValueError, KeyError):
+    WRITE_SIZE passes in profiles/hbm_traffic.json, each counter scaled by what it reads for a
+    plain copy of known size. None when that kernel has no recorded pass, or when the passes were
+    taken on other kernel sources than this build's (the file records their build stamp)."""
+    table = _traffic_table()
+    entry = table.get("kernels", {}).get(key)
+    if entry is None or table.get("build") != build_stamp():
         return None
-    return None if entry is None else entry["traffic"]
+    return entry["traffic"]
+
+
+def traffic_source() -> dict:
+    """Where roofline.traffic comes from, and whether it describes this build."""
+    recorded = _traffic_table().get("build")
+    return {"file": "profiles/hbm_traffic.json", "measured_build": recorded, "this_build": build_stamp(),
+            "fresh": recorded == build_stamp()}
+
+
+def host_info() -> dict:
+    """The host the CPU baseline ran on: its core count and the cores this process may use."""
+    return {"nproc": os.cpu_count(), "usable_cores": len(os.sched_getaffinity(0))}
 
 
 def parse() -> argparse.Namespace:
@@ -60,6 +103,11 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--headline-only", action="store_true", help="the C4 line without the C1/C2/C3/C5 workloads "
+                   "(for profiling the attention kernels alone)")
+    p.add_argument("--summarize", metavar="DIR", help="reduce the rocprofv3 CSVs in DIR (kernel traces named <workload>, "
+                   "counter passes named <workload>_<counter>) into profiles/hbm_traffic.json and print per-kernel "
+                   "tables; touches no GPU")
     p.add_argument(
         "--workload",
         default="c4",
@@ -68,6 +116,86 @@ def parse() -> argparse.Namespace:
         "known-size reference that scales rocprofv3's FETCH_SIZE/WRITE_SIZE counters",
     )
     return p.parse_args()
+
+
+def _short_kernel(name: str) -> str:
+    """A template kernel's rocprofv3 name, shortened: `sdpa_bwd_kv_dma<BF16,true,false>`."""
+    import re
+
+    m = re.search(r"(\w+_(?:mfma|dma|rows))<([^()]*)>", name)
+    if m:
+        return f"{m.group(1)}<{m.group(2).replace('limn::', '').replace(' ', '')}>"
+    return name.split("(")[0].replace("void ", "")
+
+
+def summarize(directory: str) -> int:
+    """Reduce rocprofv3 CSV output to the figures bench.py reports and profiles/ keeps.
+
+    Kernel traces `<w>_kernel_trace.csv` give per-kernel dispatch counts and durations (the last
+    10 dispatches are the bench's timed steps). Counter passes `<w>_<pass>_counter_collection.csv`
+    give per-dispatch counter values, averaged per kernel. FETCH_SIZE and WRITE_SIZE of the
+    `copy` workload (a 256 MiB copy) calibrate the HBM byte counters; every kernel with both
+    passes gets its scaled read and written bytes in profiles/hbm_traffic.json, stamped with this
+    build's kernel sources."""
+    import collections
+    import csv
+    import glob
+
+    def rows(path):
+        with open(path) as f:
+            return list(csv.DictReader(f))
+
+    traces, counters, resources = {}, collections.defaultdict(dict), {}
+    for path in sorted(glob.glob(os.path.join(directory, "*_kernel_trace.csv"))):
+        w = os.path.basename(path)[: -len("_kernel_trace.csv")]
+        d = collections.defaultdict(list)
+        for r in rows(path):
+            d[_short_kernel(r["Kernel_Name"])].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        traces[w] = d
+    for path in sorted(glob.glob(os.path.join(directory, "*_counter_collection.csv"))):
+        w = os.path.basename(path)[: -len("_counter_collection.csv")].split("_")[0]
+        acc = collections.defaultdict(list)
+        for r in rows(path):
+            k = _short_kernel(r["Kernel_Name"])
+            acc[(k, r["Counter_Name"])].append(float(r["Counter_Value"]))
+            if "VGPR_Count" in r:
+                resources[(w, k)] = (r.get("VGPR_Count"), r.get("Accum_VGPR_Count"), r.get("LDS_Block_Size"))
+        for (k, c), v in acc.items():
+            counters[w].setdefault(k, {})[c] = sum(v) / len(v)
+    out = {"build": build_stamp(), "calibration": None, "kernels": {}}
+    copy = counters.get("copy", {}).get("limn_copy_probe", {})
+    if "FETCH_SIZE" in copy and "WRITE_SIZE" in copy:
+        nb = 256 << 20
+        fs, ws = nb / (copy["FETCH_SIZE"] * 1024), nb / (copy["WRITE_SIZE"] * 1024)
+        out["calibration"] = {"kernel": "limn_copy_probe (bench.py --workload copy)", "bytes_read": nb, "bytes_written": nb,
+                              "FETCH_SIZE_KiB": round(copy["FETCH_SIZE"], 1), "WRITE_SIZE_KiB": round(copy["WRITE_SIZE"], 1),
+                              "fetch_scale": round(fs, 3), "write_scale": round(ws, 3)}
+        for w, per_kernel in counters.items():
+            for k, c in per_kernel.items():
+                # the kernels bench lines report: C4's attention passes, C2's nests, C3's contraction
+                wanted = w == "c2" or (w == "c3" and k.startswith("matmul")) or (w == "c4" and k.startswith("sdpa_"))
+                if wanted and "FETCH_SIZE" in c and "WRITE_SIZE" in c:
+                    rb, wb = c["FETCH_SIZE"] * 1024 * fs, c["WRITE_SIZE"] * 1024 * ws
+                    out["kernels"][f"{w}:{k}"] = {"FETCH_SIZE_KiB": round(c["FETCH_SIZE"], 1), "WRITE_SIZE_KiB": round(c["WRITE_SIZE"], 1),
+                                                  "read_bytes": round(rb), "written_bytes": round(wb), "traffic": round(rb + wb)}
+    for w, d in traces.items():
+        names = sorted({c for k in counters.get(w, {}).values() for c in k})
+        print(f"\n## {w}\n")
+        print("| kernel | calls | avg us | timed avg us | VGPR | AGPR | " + " | ".join(names) + " |")
+        print("|---|---|---|---|---|---|" + "---|" * len(names))
+        for k, v in sorted(d.items(), key=lambda kv: -sum(kv[1])):
+            if k.startswith("__amd"):
+                continue
+            timed = v[-10:]
+            vg, ag, _ = resources.get((w, k), ("", "", ""))
+            vals = [counters[w].get(k, {}).get(c) for c in names]
+            cells = " | ".join("" if x is None else f"{x:,.1f}" for x in vals)
+            print(f"| {k} | {len(v)} | {sum(v) / len(v):.1f} | {sum(timed) / len(timed):.1f} | {vg} | {ag} | {cells} |")
+    if out["kernels"]:
+        with open(TRAFFIC, "w") as f:
+            json.dump(out, f, indent=1)
+        print(f"\nwrote {TRAFFIC}: {len(out['kernels'])} kernels, build {out['build']}, calibration {out['calibration']}")
+    return 0
 
 
 COPY_SOURCE = """
@@ -172,6 +300,7 @@ def c4_cpu_baseline(host, scale: float, B: int, H: int, units: float) -> dict:
         "unit": "TFLOP/s",
         "cores": 1,
         "kind": "port",
+        "host": host_info(),
         "sample": f"C device (limn/backend_c.py restated, gcc -O3, 1 thread), float32 twin, composed causal attention "
         f"fwd+bwd on 1 of {B * H} (b,h) pairs: {one:.2f} s in compiled nests, scaled x{B * H}",
     }
@@ -201,6 +330,7 @@ def cpu_baseline(q, k, v, do, scale: float, B: int, H: int, units: float) -> dic
         "unit": "TFLOP/s",
         "cores": int(cores),
         "kind": "port",
+        "host": host_info(),
         "sample": f"numpy oracle (limn/sdpa.py port, block 16) fwd+bwd on 1 of {B * H} (b,h) pairs, {one:.2f} s, scaled x{B * H}",
     }
 
@@ -320,12 +450,14 @@ def bench_c2(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK, 4),
             "traffic": traffic(f"c2:k{dom}"),
+            "traffic_source": traffic_source(),
         },
         "cpu_baseline": None if cpu_s is None else {
             "value": round(total / cpu_s / 1e9, 3),
             "unit": "GB/s",
             "cores": 1,
             "kind": "port",
+            "host": host_info(),
             "sample": f"C device (limn/backend_c.py restated, gcc -O3, 1 thread), the same 11 scheduled kernels at full size: {cpu_s:.2f} s",
         },
     }
@@ -388,12 +520,14 @@ def bench_c3(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
             "unit": "TFLOP/s",
             "frac": round(flops / (mm * 1e-3) / MFMA_BF16_PEAK, 4),
             "traffic": traffic("c3:matmul_dma<BF16,256,256,true,false,1,false>"),
+            "traffic_source": traffic_source(),
         },
         "cpu_baseline": None if cpu_s is None else {
             "value": round(2.0 * rows * n * n / cpu_s / 1e12, 6),
             "unit": "TFLOP/s",
             "cores": 1,
             "kind": "port",
+            "host": host_info(),
             "sample": f"C device (limn/backend_c.py restated, gcc -O3, 1 thread), float32 twin, (A[:{rows}] @ B).relu(): {cpu_s:.2f} s",
         },
     }
@@ -471,6 +605,7 @@ def bench_c1(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
             "unit": "us",
             "cores": 1,
             "kind": "port",
+            "host": host_info(),
             "sample": f"C device (limn/backend_c.py restated, gcc -O3, 1 thread), composed causal attention fwd+bwd, full C1: {cpu_s * 1e3:.1f} ms",
         },
     }
@@ -532,6 +667,7 @@ def bench_c5(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
             "unit": "tok/s",
             "cores": 1,
             "kind": "port",
+            "host": host_info(),
             "sample": f"C device (limn/backend_c.py restated, gcc -O3, 1 thread), float32 twin, one training step of "
             f"batch 1 ({twin.tokens} tokens, composed attention): {cdev.seconds:.1f} s in compiled nests",
         }
@@ -558,6 +694,8 @@ def main() -> int:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (every box has one MI355X)", file=sys.stderr)
         return 2
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    if args.summarize:
+        return summarize(args.summarize)
     if args.workload == "copy":
         return copy_probe(args.steps)
     if args.workload == "c1":
@@ -583,7 +721,7 @@ def main() -> int:
     from limn_amd.dtypes import bf16_bits, bf16_values
     from limn_amd.hip.device import HipDevice
     from limn_amd.hip.runtime import hip_unavailable
-    from limn_amd.seam import Node, Op, bfloat16, custom, float32
+    from limn_amd.seam import Node, Op, Tensor, bfloat16, custom, float32, topological
 
     reason = hip_unavailable()
     if reason is not None:
@@ -605,9 +743,17 @@ def main() -> int:
     out, lse = dev.out_alloc(B * H * S * D * 2, False), dev.out_alloc(B * H * S * 4, False)
     fwd([q.arg, k.arg, v.arg], [out, lse])
     dev.finish()
-    o_host = bf16_values(dev.copyout(out).view(np.uint16).reshape(B, H, S, D))
-    delta_host = (bf16_values(host[3].reshape(B, H, S, D)) * o_host).sum(axis=-1, keepdims=True).astype(np.float32)
-    delta = buffer(delta_host, float32, (B, H, S, 1))
+    # delta = rowsum(dO * O) in float32, spelled as limn's backward spells it (reference
+    # limn/tensor.py:702-707): one emitted SUM nest, run by the device's own runner
+    o_t = Tensor.from_node(Node(Op.BUFFER, (), bfloat16, (B, H, S, D), out))
+    delta_node = (Tensor.from_node(do).cast(float32) * o_t.cast(float32)).sum(axis=-1, keepdim=True).node
+    order = topological([delta_node])
+    delta_plan = dev.plan_of(order, {n: i for i, n in enumerate(order)}, [delta_node])
+    assert len(delta_plan.calls) == 1, "the delta row-dot is one nest"
+    delta_fn, delta_ins = delta_plan.calls[0].fn, [order[p].arg for p in delta_plan.calls[0].inputs]
+    delta_buf = dev.out_alloc(B * H * S * 4, False)
+    delta_fn(delta_ins, [delta_buf])
+    delta = Node(Op.BUFFER, (), float32, (B, H, S, 1), delta_buf)
     lse_node = Node(Op.BUFFER, (), float32, (B, H, S, 1), lse)
     srcs = (q, k, v, do, lse_node, delta)
     (dq_node,) = custom("sdpa_bwd_q", srcs, (True, scale), ((bfloat16, (B, H, S, D)),))
@@ -617,39 +763,41 @@ def main() -> int:
     ins_fwd = [q.arg, k.arg, v.arg]
     ins_bwd = [q.arg, k.arg, v.arg, do.arg, lse, delta.arg]
 
-    def step():
-        fwd(ins_fwd, [out, lse])
-        bwd_q(ins_bwd, [dq])
-        bwd_kv(ins_bwd, [dk, dv])
-
+    stages = (
+        lambda: fwd(ins_fwd, [out, lse]),
+        lambda: delta_fn(delta_ins, [delta_buf]),
+        lambda: bwd_q(ins_bwd, [dq]),
+        lambda: bwd_kv(ins_bwd, [dk, dv]),
+    )
     for _ in range(args.warmup):
-        step()
+        for stage in stages:
+            stage()
     dev.finish()
-    ev = Events(dev.api, 2 + 4 * args.steps)
-    per = np.zeros(3)
+    per_step = len(stages) + 1
+    ev = Events(dev.api, 2 + per_step * args.steps)
+    per = np.zeros(len(stages))
     ev.record(0)
     for s in range(args.steps):
-        base = 2 + 4 * s
-        ev.record(base)
-        fwd(ins_fwd, [out, lse])
-        ev.record(base + 1)
-        bwd_q(ins_bwd, [dq])
-        ev.record(base + 2)
-        bwd_kv(ins_bwd, [dk, dv])
-        ev.record(base + 3)
+        base = 2 + per_step * s
+        for i, stage in enumerate(stages):
+            ev.record(base + i)
+            stage()
+        ev.record(base + len(stages))
     ev.record(1)
     dev.finish()
     total_ms = ev.ms(0, 1)
     for s in range(args.steps):
-        base = 2 + 4 * s
-        per += [ev.ms(base, base + 1), ev.ms(base + 1, base + 2), ev.ms(base + 2, base + 3)]
+        base = 2 + per_step * s
+        per += [ev.ms(base + i, base + i + 1) for i in range(len(stages))]
     per /= args.steps
     ms = total_ms / args.steps
 
     U = 2.0 * B * H * S * S * D / 2
     step_flops = 7 * U
-    kernel_flops = {"sdpa": 2 * U, "sdpa_bwd_q": 1 * U, "sdpa_bwd_kv": 4 * U}
-    names = ["sdpa", "sdpa_bwd_q", "sdpa_bwd_kv"]
+    kernel_flops = {"sdpa": 2 * U, "delta": 0.0, "sdpa_bwd_q": 1 * U, "sdpa_bwd_kv": 4 * U}
+    names = ["sdpa", "delta", "sdpa_bwd_q", "sdpa_bwd_kv"]
+    delta_bytes = 2 * B * H * S * D * 2 + B * H * S * 4  # dO and O read, delta written
+    custom_ms = float(per[0] + per[2] + per[3])
     # the template instance each CUSTOM name runs at this configuration (rocprofv3's kernel names)
     KERNEL_SYMBOL = {
         "sdpa": "sdpa_fwd_dma<BF16,true,false>",
@@ -683,6 +831,17 @@ def main() -> int:
         },
         "mfma_peak_frac": round(value / MFMA_BF16_PEAK, 4),
         "kernels_ms": {n: round(float(t), 4) for n, t in zip(names, per)},
+        "custom_kernels": {
+            "note": "the three CUSTOM kernels alone, the north star's 40% target (the step adds the delta nest)",
+            "ms": round(custom_ms, 4),
+            "mfma_peak_frac": round(step_flops / (custom_ms * 1e-3) / MFMA_BF16_PEAK, 4),
+        },
+        "delta_kernel": {
+            "ms": round(float(per[1]), 4),
+            "bytes": delta_bytes,
+            "GB_s": round(delta_bytes / (per[1] * 1e-3) / 1e9, 1),
+            "hbm_frac": round(delta_bytes / (per[1] * 1e-3) / HBM_PEAK, 4),
+        },
         "roofline": {
             "kernel": names[dom],
             "bound": "mfma",
@@ -691,6 +850,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_BF16_PEAK, 4),
             "traffic": traffic(f"c4:{KERNEL_SYMBOL[names[dom]]}"),
+            "traffic_source": traffic_source(),
         },
         "device": {"arch": dev.arch, "compute_units": dev.compute_units},
     }
@@ -698,8 +858,11 @@ def main() -> int:
         line["cpu_baseline"] = c4_cpu_baseline(host, scale, B, H, step_flops)
         inputs = [bf16_values(h.reshape(B, H, S, D)[:1, :1]) for h in host]
         line["cpu_numpy_oracle"] = cpu_baseline(*inputs, scale, B, H, step_flops)
-    del q, k, v, do, out, lse, dq, dk, dv, delta, lse_node, o_node, l_node, dq_node, dk_node
+    del q, k, v, do, out, lse, dq, dk, dv, delta, lse_node, o_node, l_node, dq_node, dk_node, delta_buf, delta_ins, o_t
     cpu = not args.no_cpu
+    if args.headline_only:
+        print(json.dumps(line), flush=True)
+        return 0
     line["workloads"] = {
         "C1": bench_c1(dev, args.steps, args.warmup, cpu),
         "C2": bench_c2(dev, args.steps, args.warmup, cpu),
