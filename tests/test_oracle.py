@@ -95,16 +95,21 @@ def _check_cases():
         (q, k, v, np.broadcast_to(pad, (2, 3, 128)).astype(np.float32), True, 1e-5, "float32"),
         (q, k, v, holes, False, 1e-5, "float32"),
         (r(4, 1, 32), r(4, 96, 32), r(4, 96, 48), np.broadcast_to(np.arange(96) < 61, (4, 96)).astype(np.float32), False, 1e-5, "float32"),
+        # the half widths: inputs rounded to storage, the textbook form run widened on those values
+        (*(r(*s).astype(np.float16).astype(np.float32) for s in ((2, 3, 128, 32), (2, 3, 128, 32), (2, 3, 128, 48))), None, True, 2e-3, "float16"),
+        (*(bf16.rne(r(*s)) for s in ((2, 3, 128, 32), (2, 3, 128, 32), (2, 3, 128, 48))), None, True, 2e-2, "bfloat16"),
     ]
 
 
-@pytest.mark.parametrize("case", range(9))
+@pytest.mark.parametrize("case", range(11))
 def test_blocked_recurrence_equals_the_textbook_form(case):
-    """limn/sdpa.py's check(): every block size (1, 16, t, t+7) lands on the materialized form."""
+    """limn/sdpa.py's check(): every block size (1, 16, t, t+7) lands on the materialized form,
+    for all eleven of its cases (f32, f64, f16, bf16, masks, ragged and rectangular shapes)."""
     q, k, v, mask, causal, tol, dtype = _check_cases()[case]
     rng = np.random.default_rng(case)
     scale = q.shape[-1] ** -0.5
     do = rng.standard_normal(q.shape[:-1] + v.shape[-1:]).astype(q.dtype)
+    stored_do = ref.store(do, dtype).astype(q.dtype)  # the backward reads dO at the storage width
     want = ref.plain(q, k, v, causal=causal, scale=scale, key_mask=mask)
     want_grads = ref.plain_backward(q, k, v, do, causal=causal, scale=scale, key_mask=mask)
     for block in (1, 16, k.shape[-2], k.shape[-2] + 7):
@@ -112,7 +117,7 @@ def test_blocked_recurrence_equals_the_textbook_form(case):
         assert ref.worst(out, want) <= tol
         assert ref.worst(lse, ref.plain_lse(q, k, causal=causal, scale=scale, key_mask=mask)) <= tol
         delta = (do * out).sum(axis=-1, keepdims=True)
-        args = (q, k, v, do, lse, delta, mask)
+        args = (q, k, v, stored_do, lse, delta, mask)
         dq = ref.sdpa_backward_q(*args, causal=causal, scale=scale, dtype=dtype, block_size=block)
         dk, dv = ref.sdpa_backward_kv(*args, causal=causal, scale=scale, dtype=dtype, block_size=block)
         for got, w in zip((dq, dk, dv), want_grads):
