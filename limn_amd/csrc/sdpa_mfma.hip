@@ -862,12 +862,22 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_dma(const u16* __restr
   const int qstart = CAUSAL ? k0 : 0;  // a causal key is seen by queries at or after it
   const int ntiles = qstart < t_q ? (t_q - qstart + TILE - 1) / TILE : 0;
 
-  // a tile's statistics (lse * log2 e and delta * scale of its queries), by the first wave
-  auto stats = [&](int r0, float* L, float* Dl) __attribute__((always_inline)) {
+  // a tile's statistics (lse * log2 e and delta * scale of its queries), by the first wave: loaded
+  // into registers when the tile's copy starts and stored into LDS only after the tile before it
+  // is computed. Loads retire in order, so using them sooner would wait for the whole copy first.
+  float next_l = 0.f, next_d = 0.f;
+  auto stats_load = [&](int r0) __attribute__((always_inline)) {
     if (threadIdx.x < TILE) {
       const int qq = r0 + (int)threadIdx.x;
-      L[threadIdx.x] = qq < t_q ? lse[b * (int64_t)t_q + qq] * LOG2E : 0.f;
-      Dl[threadIdx.x] = qq < t_q ? delta[b * (int64_t)t_q + qq] * scale : 0.f;
+      next_l = qq < t_q ? lse[b * (int64_t)t_q + qq] : 0.f;
+      next_d = qq < t_q ? delta[b * (int64_t)t_q + qq] : 0.f;
+    }
+  };
+  auto stats_store = [&](float* L, float* Dl) __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);  // keeps the scaling (the loads' first use) below the compute
+    if (threadIdx.x < TILE) {
+      L[threadIdx.x] = next_l * LOG2E;
+      Dl[threadIdx.x] = next_d * scale;
     }
   };
   // tile it from (Qc, Oc, Lc, Dc) while tile it + 1 is copied into the idle buffers (every wave
@@ -877,8 +887,9 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_dma(const u16* __restr
     const int r0 = qstart + it * TILE;
     qd.copy(Qn, r0 + TILE, wave);
     od.copy(On, r0 + TILE, wave);
-    stats(r0 + TILE, Ln, Dn);
+    stats_load(r0 + TILE);
     kv_tile128<T, CAUSAL, MASK, decltype(edge)::value>(Qc, Oc, Lc, Dc, ad, r0, wk0, t_q, c2, scale, live, kf, vf, gk, gv);
+    stats_store(Ln, Dn);
     __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
     __syncthreads();
   };
@@ -894,7 +905,8 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_dma(const u16* __restr
   if (ntiles > 0) {
     qd.copy(Q0, qstart, wave);
     od.copy(O0, qstart, wave);
-    stats(qstart, L0, D0);
+    stats_load(qstart);
+    stats_store(L0, D0);
     __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
     __syncthreads();
   }

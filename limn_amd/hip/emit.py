@@ -23,10 +23,12 @@ one-thread-per-cell launch):
 - few cells over a long reduce (the reference's split reduce, limn/cuda_emit.py:134-149):
   PARTS workgroups per cell write partials to a scratch buffer, and a second kernel folds each
   cell's partials in index order;
-- a float SCATTER (float32, float64) gives np.add.at's bits: a tiled sort of the occurrences by
-  row, then a workgroup per (row, 64 columns) adds that row's values in occurrence order
-  (`plan_scatter`). An int32 SCATTER adds with hardware atomics, which is exact in any order.
-  Like the reference's GPU device, the half widths and narrow ints are refused.
+- a float SCATTER gives np.add.at's bits: a tiled sort of the occurrences by row, then a
+  workgroup per (row, 64 columns) adds that row's values in occurrence order (`plan_scatter`);
+  float16 and bfloat16 tables round their running totals to their own width after every add,
+  as np.add.at into a half-width array does (the reference's GPU device declines them). An
+  int32 SCATTER adds with hardware atomics, which is exact in any order. The narrow ints are
+  refused, as the reference's GPU device refuses them.
 """
 
 from __future__ import annotations
@@ -542,7 +544,7 @@ def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned
         lines.append("      " + value_line(instr, bufs))
     buf, index = write.arg
     if write.opcode is Opcode.SCATTER:
-        if out_dtype not in (float32, float64, int32):
+        if out_dtype not in (float32, float64, float16, bfloat16, int32):
             raise NotImplementedError(f"the hip device cannot scatter {out_dtype}; cast the table to float32 or int32")
         if out_dtype != int32:
             return plan_scatter(nest, shape, bufs)
@@ -616,7 +618,12 @@ def plan_scatter(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
       ones as 0.
 
     FMA contraction is off in the accumulating kernel so a value computed by a product is
-    rounded before it is added, as numpy rounds it."""
+    rounded before it is added, as numpy rounds it. A float16 or bfloat16 table keeps its
+    running total at its own width, rounded to nearest even after every add, which is what
+    np.add.at into a half-width array does (the reference's oracle zero-fills the table at the
+    node's dtype); the values themselves are the kernel's float32 results, so a scatter of
+    loaded half-width values matches bit for bit and one of fused half-width arithmetic to the
+    half-width tolerance."""
     out_dtype = nest.kernel.target.dtype
     table = nest.kernel.target.shape
     if len(table) != 2:
@@ -640,7 +647,8 @@ def plan_scatter(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     if any(col_var in _reads(i) for i in key_body):
         raise NotImplementedError("a scatter row index that depends on the column")
     value_body = _needed(shape.body, {write.srcs[0]})
-    acc_t = STORE_T[out_dtype]
+    half = out_dtype in (float16, bfloat16)
+    acc_t = "float" if half else STORE_T[out_dtype]
     tile = next((t for limit, t in SORT_TILE_LIMITS if occurrences <= limit), SORT_TILE_MAX)
     tiles = max(1, -(-occurrences // tile))
     block = 64  # one wave: the scan and the tile search below are lane-wide
@@ -708,7 +716,7 @@ def plan_scatter(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     sort.append(f"  for (int e_ = 0; e_ < {per}; e_++) runs[base_ + th_ * {per} + e_] = x_[e_];")
     sort.append("}")
 
-    acc = [f'extern "C" __global__ __launch_bounds__({block}) void {nest.name}({", ".join(params + ["const unsigned long long* __restrict__ ALIGNED runs", f"{acc_t}* __restrict__ ALIGNED out"])}) {{']
+    acc = [f'extern "C" __global__ __launch_bounds__({block}) void {nest.name}({", ".join(params + ["const unsigned long long* __restrict__ ALIGNED runs", f"{STORE_T[out_dtype]}* __restrict__ ALIGNED out"])}) {{']
     acc.append("#pragma clang fp contract(off)")
     acc.append("  __shared__ int lo_[64], start_[64];")
     acc.append(f"  __shared__ unsigned list_[{LIST_CAP}];")
@@ -751,14 +759,17 @@ def plan_scatter(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
     acc.append("        const i64 o_ = (i64)list_[j_];")
     acc += decode(lead, "o_", "        ", True)
     acc += ["        " + value_line(i, bufs) for i in value_body]
-    acc.append(f"        acc_ += ({acc_t}){write.srcs[0]};")
+    if half:  # the table's own width after every add, as np.add.at into a half array rounds
+        acc.append(f"        acc_ = {load_expr(out_dtype, store_expr(out_dtype, f'acc_ + (float){write.srcs[0]}'))};")
+    else:
+        acc.append(f"        acc_ += ({acc_t}){write.srcs[0]};")
     acc.append("      }")
     acc.append("    }")
     acc.append("  }")
     acc.append(f"  if (c_ < {cols}) {{")
     if row_name:
         acc.append(f"    const int {row_name} = r_;")
-    acc.append(f"    out[{render_index(index, True)}] = acc_;")
+    acc.append(f"    out[{render_index(index, True)}] = {store_expr(out_dtype, 'acc_') if half else 'acc_'};")
     acc.append("  }")
     acc.append("  }")
     acc.append("}")

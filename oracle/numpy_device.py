@@ -66,6 +66,18 @@ def materialize(view: "view.View", flat: np.ndarray) -> np.ndarray:
     return np.where(ok, flat[np.clip(idx, 0, flat.size - 1)], np.zeros((), dtype=flat.dtype))
 
 
+def scatter_rounding_each_add(table: np.ndarray, indices: np.ndarray, values: np.ndarray) -> None:
+    """np.add.at into a bfloat16 table (reference limn/device.py:155-157, a table of the node's
+    own dtype): occurrences in order, each add done in float32 and rounded to bfloat16 at once,
+    as ml_dtypes' add does. `table` holds bfloat16 values as float32."""
+    rows = table.shape[0]
+    flat_idx = np.asarray(indices).reshape(-1)
+    flat_val = np.asarray(values, dtype=np.float32).reshape(flat_idx.size, *table.shape[1:])
+    for j, r in enumerate(flat_idx):
+        r = int(r) + rows if r < 0 else int(r)
+        table[r] = bf16.rne(table[r] + flat_val[j])
+
+
 def read_buffer(buf: np.ndarray, dtype: DType, shape) -> np.ndarray:
     raw = buf.view(STORAGE[dtype]).reshape(shape)
     return bf16.widen(raw) if dtype == bfloat16 else raw
@@ -158,7 +170,10 @@ class NumpyDevice(HostDevice):
                 result = srcs[0][srcs[1]]
             elif op is Op.SCATTER:
                 result = np.zeros(node.shape, dtype=COMPUTE[node.dtype])
-                np.add.at(result, srcs[0], srcs[1])
+                if node.dtype == bfloat16:
+                    scatter_rounding_each_add(result, srcs[0], srcs[1])
+                else:  # float16 arithmetic already rounds every add, as limn's half array does
+                    np.add.at(result, srcs[0], srcs[1])
             elif op is Op.CONTIGUOUS:
                 result = np.ascontiguousarray(srcs[0])
             elif op is Op.CUSTOM:

@@ -212,10 +212,22 @@ def test_scatter_int32_is_exact(hipdev):
     check(hipdev, scatter_rows(values, idx, (6, 5)), exact=True)
 
 
-def test_scatter_refuses_half_widths(hipdev):
+@pytest.mark.parametrize("dtype", [bfloat16, float16], ids=["bfloat16", "float16"])
+def test_half_width_scatter_rounds_each_add(hipdev, dtype):
+    """A half-width table at the GPT's token-table shape (16384 occurrences into 256 rows of 512):
+    np.add.at into a half array rounds the running total after every add, so the kernel's bits
+    must equal the oracle's, which would not hold for a float32 total rounded once."""
     from limn_amd.seam import scatter_rows
 
-    values = Tensor(randf(8, 4), dtype=bfloat16)
+    values = Tensor(order_sensitive(32, 512, 512), dtype=dtype)
+    idx = Tensor(rng.integers(-256, 256, size=(32, 512)).astype(np.int32))
+    check(hipdev, scatter_rows(values, idx, (256, 512)), bitwise=True)
+
+
+def test_scatter_refuses_narrow_ints(hipdev):
+    from limn_amd.seam import scatter_rows
+
+    values = Tensor(rng.integers(-5, 5, size=(8, 4)).astype(np.int8), dtype=int8)
     idx = Tensor(np.zeros(8, dtype=np.int32))
     with pytest.raises(NotImplementedError):
         hipdev.execute([scatter_rows(values, idx, (2, 4)).node])

@@ -146,3 +146,17 @@ def test_each_replay_returns_its_own_tensor():
     fourth = fn(Tensor(np.full(4, 2.0, dtype=np.float32)))
     assert third is not fourth
     assert (third.item(), fourth.item()) == (8.0, 12.0)
+
+
+def test_a_bfloat16_scatter_rounds_every_add():
+    """np.add.at into limn's bfloat16 table (reference limn/device.py:155-157) adds in float32 and
+    rounds to bfloat16 after every add: at 256 the bf16 spacing is 2, so each 0.5 rounds away and
+    the row stays 256, where a float32 total rounded once would give 258."""
+    from limn_amd.seam import scatter_rows
+
+    values = np.array([[256.0], [0.5], [0.5], [0.5], [0.5], [3.0]], dtype=np.float32)
+    idx = np.array([0, 0, 0, 0, 0, 1], dtype=np.int32)
+    got = scatter_rows(Tensor(values, dtype=bfloat16), Tensor(idx), (2, 1)).numpy()
+    np.testing.assert_array_equal(got, np.array([[256.0], [3.0]], np.float32))
+    halves = scatter_rows(Tensor(values, dtype=float16), Tensor(idx), (2, 1)).numpy()  # spacing 0.25 at 256
+    np.testing.assert_array_equal(halves, np.array([[258.0], [3.0]], np.float16))
