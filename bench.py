@@ -637,11 +637,13 @@ def bench_c5(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
             loss = fn(*batches[i % 4])
         first_loss = float(loss.item())
         dev.finish()
+        issued = dev.issue_seconds
         t0 = time.perf_counter()
         for i in range(steps):
             loss = fn(*batches[i % 4])
         dev.finish()
         elapsed = time.perf_counter() - t0
+        issue_ms = (dev.issue_seconds - issued) / steps * 1e3
         last_loss = float(loss.item())
     finally:
         limn_device.active_device = saved
@@ -681,6 +683,7 @@ def bench_c5(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
                    "tokens_per_step": cfg.tokens, "flop_per_step": per_step, "params_in_matmuls": cfg.matmul_params()},
         "mfu": round(per_step * steps / elapsed / MFMA_BF16_PEAK, 4),
         "loss": {"after_warmup": round(first_loss, 4), "last": round(last_loss, 4)},
+        "host_issue_ms_per_step": round(issue_ms, 3),
         "roofline": {"kernel": "whole step", "bound": "mfma", "achieved": round(per_step * steps / elapsed / 1e12, 2),
                      "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s", "frac": round(per_step * steps / elapsed / MFMA_BF16_PEAK, 4),
                      "traffic": None},

@@ -129,6 +129,45 @@ int limn_hip_matmul_noalloc(const void* a, const void* b, void* c, int dtype, in
 int limn_hip_matmul_supported(int dtype, int64_t M, int64_t N, int64_t K, int64_t a_batch, int64_t a_m, int64_t a_k,
                               int64_t b_batch, int64_t b_k, int64_t b_n);
 
+/*
+ * A pre-bound launch list: the kernels of one recorded execution of a plan, replayed against new
+ * buffers. Each step is one launch: a hipRTC module kernel (`function`, `grid` x `block`
+ * threads, its arguments the kernel's parameters in order), a zero fill (pointer, bytes), or one
+ * call of limn_hip_matmul (its 20 arguments before `stream`), limn_hip_sdpa_fwd (13 before
+ * `scale`), limn_hip_sdpa_bwd_q (15) or limn_hip_sdpa_bwd_kv (16), with `scale` in the step. An
+ * argument is `value` when `slot` < 0, else slots[slot] + value: a byte offset into the buffer
+ * this replay binds to that slot. Steps run in order on `stream`; the first failing one stops the
+ * list and its status is returned. No counterpart in the reference: its capture replays a plan
+ * by calling every kernel's runner again (limn/capture.py:152-179).
+ */
+enum {
+  LIMN_HIP_STEP_KERNEL = 0,
+  LIMN_HIP_STEP_ZERO = 1,
+  LIMN_HIP_STEP_MATMUL = 2,
+  LIMN_HIP_STEP_SDPA_FWD = 3,
+  LIMN_HIP_STEP_SDPA_BWD_Q = 4,
+  LIMN_HIP_STEP_SDPA_BWD_KV = 5,
+};
+
+typedef struct {
+  int64_t value;
+  int32_t slot;
+  int32_t reserved;
+} limn_hip_replay_arg;
+
+typedef struct {
+  int32_t kind;
+  int32_t nargs;
+  int64_t first; /* this step's arguments are args[first .. first + nargs) */
+  void* function;
+  int32_t grid;
+  int32_t block;
+  double scale;
+} limn_hip_replay_step;
+
+int limn_hip_replay(const limn_hip_replay_step* steps, int64_t nsteps, const limn_hip_replay_arg* args, int64_t nargs,
+                    const int64_t* slots, int64_t nslots, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

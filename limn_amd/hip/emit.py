@@ -39,7 +39,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from limn_amd.hip import runtime
+from limn_amd.hip import replay, runtime
 from limn_amd.seam import DType, Index, Instr, LoopNest, Op, Opcode, Valid, accumulate_in, bfloat16, float16, float32, float64, int8, int16, int32
 
 THREADS = 256
@@ -1108,6 +1108,8 @@ def _launcher(dev, fn: int, launch: Launch, nin: int):
         for k, p in enumerate(ptrs):
             slots[k] = p
         runtime.check(api.hipModuleLaunchKernel(fn, grid, 1, 1, block, 1, 1, 0, None, params, None), f"launching {launch.name}")
+        if dev.tape is not None:
+            dev.tape.append(replay.Launch(replay.STEP_KERNEL, tuple(ptrs), function=fn, grid=grid, block=block))
 
     return run
 
@@ -1538,6 +1540,8 @@ def _matmul_launcher(dev, con: Contraction, epilogue: int):
         b = inputs[con.b_input].ptr + con.b_offset * size
         ws = held[0].ptr if held else None
         runtime.check_limn(lib.limn_hip_matmul(a, b, out, *shape, ws, ws_bytes, None))
+        if dev.tape is not None:
+            dev.tape.append(replay.Launch(replay.STEP_MATMUL, (a, b, out, *shape, ws, ws_bytes)))
 
     return launch
 

@@ -1,0 +1,93 @@
+"""Pre-bound launch lists: a plan's launches recorded once, replayed by one native call.
+
+The executor runs a plan call by call, and each call's runner rebuilds its launch arguments in
+Python (reference `limn/jit.py:159-184`; capture replays through the same `run`,
+`limn/capture.py:152-179`). A training step is hundreds of launches, so that host work is
+milliseconds per step. The hip device instead records a hot plan's launches once, during an
+ordinary run with every buffer of the run kept alive: each launch becomes a step of
+`limn_hip_replay` (include/limn_hip.h) and each argument either a constant (a size, a kernel's
+own scratch pointer) or an offset into a *slot*: a buffer position of the plan (its sources) or
+one of the outputs the run allocated, in call order. A replay allocates fresh outputs, binds every
+slot to this run's buffer and issues the whole list in one call.
+
+A recording is refused (the plan keeps running call by call) when two slots share bytes, since a
+pointer into them could not be told apart.
+"""
+
+from __future__ import annotations
+
+import bisect
+from dataclasses import dataclass
+
+import numpy as np
+
+STEP_KERNEL, STEP_ZERO, STEP_MATMUL, STEP_SDPA_FWD, STEP_SDPA_BWD_Q, STEP_SDPA_BWD_KV = range(6)
+
+# which arguments of each step kind are device pointers (the rest are sizes, codes and flags)
+POINTER_ARGS = {
+    STEP_ZERO: frozenset({0}),
+    STEP_MATMUL: frozenset({0, 1, 2, 18}),
+    STEP_SDPA_FWD: frozenset(range(6)),
+    STEP_SDPA_BWD_Q: frozenset(range(8)),
+    STEP_SDPA_BWD_KV: frozenset(range(9)),
+}
+
+ARG = np.dtype([("value", np.int64), ("slot", np.int32), ("reserved", np.int32)])
+STEP = np.dtype([("kind", np.int32), ("nargs", np.int32), ("first", np.int64), ("function", np.uint64),
+                 ("grid", np.int32), ("block", np.int32), ("scale", np.float64)])
+assert ARG.itemsize == 16 and STEP.itemsize == 40
+
+
+@dataclass(frozen=True)
+class Launch:
+    """One recorded launch: its kind, module function (kernels), grid and block, sdpa scale, and
+    its arguments as the recording run passed them."""
+
+    kind: int
+    args: tuple[int, ...]
+    function: int = 0
+    grid: int = 0
+    block: int = 0
+    scale: float = 0.0
+
+
+@dataclass
+class Program:
+    steps: np.ndarray
+    args: np.ndarray
+    out_nbytes: tuple[int, ...]  # the outputs a replay allocates, in call order
+    out_positions: tuple[tuple[int, int], ...]  # (output index, plan position) of outputs the plan reads
+    assigns: tuple[tuple[int, int], ...]  # (target position, output index) committed after the list
+    positions: int  # slots [0, positions) are the plan's buffer positions, then the outputs
+
+    @property
+    def nslots(self) -> int:
+        return self.positions + len(self.out_nbytes)
+
+    def launch(self, lib, slots: np.ndarray, stream=None) -> int:
+        return lib.limn_hip_replay(self.steps.ctypes.data, len(self.steps), self.args.ctypes.data, len(self.args),
+                                   slots.ctypes.data, len(slots), stream)
+
+
+def bind(tape: list[Launch], slots: list[tuple[int, int, int]]) -> tuple[np.ndarray, np.ndarray] | None:
+    """The recorded launches as (steps, args) arrays. `slots` holds (slot, device pointer, bytes)
+    for every buffer of the recording run; a pointer argument inside one becomes that slot plus an
+    offset, any other is kept as it is. None when two slots overlap."""
+    spans = sorted((ptr, ptr + max(nb, 1), slot) for slot, ptr, nb in slots)
+    starts = [s for s, _, _ in spans]
+    if any(a[1] > b[0] for a, b in zip(spans, spans[1:])):
+        return None
+    steps = np.zeros(len(tape), dtype=STEP)
+    rows: list[tuple[int, int, int]] = []
+    for i, launch in enumerate(tape):
+        pointers = POINTER_ARGS.get(launch.kind)
+        steps[i] = (launch.kind, len(launch.args), len(rows), launch.function, launch.grid, launch.block, launch.scale)
+        for k, value in enumerate(launch.args):
+            value = int(value or 0)
+            slot = -1
+            if (pointers is None or k in pointers) and value:
+                j = bisect.bisect_right(starts, value) - 1
+                if j >= 0 and value < spans[j][1]:
+                    slot, value = spans[j][2], value - spans[j][0]
+            rows.append((value, slot, 0))
+    return steps, np.array(rows, dtype=ARG) if rows else np.zeros(1, dtype=ARG)

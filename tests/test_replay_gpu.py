@@ -1,0 +1,69 @@
+"""Pre-bound launch lists on the MI355X: a plan's first run goes call by call, its second also
+records every launch, later runs replay the list in one native call (limn_amd/hip/replay.py).
+Each case runs one graph structure four times with new inputs and checks every result bit for bit
+against a device made to run call by call, covering emitted nests with inlined producers, an
+ordered scatter (a zero-filled output), a contraction with its relu epilogue, and attention
+forward and backward (CUSTOM calls, merged launches)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from limn_amd.seam import CompiledDevice, Tensor, bfloat16, grad, nn, realize, scatter_rows
+from limn_amd.seam import device as limn_device
+
+pytestmark = pytest.mark.gpu
+
+
+def softmax_layernorm(seed):
+    x = Tensor(np.random.default_rng(seed).standard_normal((300, 257)).astype(np.float32))
+    return [nn.LayerNorm(257)(x.softmax(-1))]
+
+
+def scatter(seed):
+    r = np.random.default_rng(seed)
+    values = Tensor(r.standard_normal((600, 40)).astype(np.float32))
+    return [scatter_rows(values, Tensor(r.integers(0, 50, 600).astype(np.int32)), (50, 40))]
+
+
+def matmul_relu(seed):
+    r = np.random.default_rng(seed)
+    a = Tensor(r.standard_normal((256, 512)).astype(np.float32), dtype=bfloat16)
+    b = Tensor(r.standard_normal((512, 384)).astype(np.float32), dtype=bfloat16)
+    return [(a @ b).relu()]
+
+
+def attention(seed):
+    r = np.random.default_rng(seed)
+    q, k, v = (Tensor(r.standard_normal((2, 2, 200, 64)).astype(np.float32), dtype=bfloat16, requires_grad=True) for _ in range(3))
+    w = Tensor(r.standard_normal((2, 2, 200, 64)).astype(np.float32))
+    out = q.attention(k, v, causal=True)
+    return [out, *grad((out.float() * w).sum(), [q, k, v])]
+
+
+CASES = {"softmax_layernorm": softmax_layernorm, "scatter": scatter, "matmul_relu": matmul_relu, "attention": attention}
+
+
+def results(dev, build, seed) -> list[np.ndarray]:
+    limn_device.active_device = dev
+    tensors = build(seed)
+    realize(*tensors)
+    return [t.numpy() for t in tensors]
+
+
+@pytest.mark.parametrize("case", sorted(CASES))
+def test_replayed_runs_equal_call_by_call_runs(hipdev, case):
+    from limn_amd.hip.device import HipDevice
+
+    plain = HipDevice()
+    plain.run = lambda plan, sources: CompiledDevice.run(plain, plan, sources)  # never records
+    before = sum(e[1] is not None for e in hipdev.replays.values())
+    for seed in range(4):
+        print(f"replay case {case}, run {seed}", flush=True)
+        got = results(hipdev, CASES[case], seed)
+        want = results(plain, CASES[case], seed)
+        for g, w in zip(got, want):
+            assert g.dtype == w.dtype and g.shape == w.shape
+            np.testing.assert_array_equal(g.view(np.uint8), w.view(np.uint8))
+    assert sum(e[1] is not None for e in hipdev.replays.values()) > before  # a list was recorded and replayed
