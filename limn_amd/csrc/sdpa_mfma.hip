@@ -950,6 +950,260 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_dma(const u16* __restr
   store_transposed<T, D>(dv + b * (int64_t)t_k * D, gv, key, t_k, 1.f);
 }
 
+// ---- dK/dV pass at D = 128 without a key mask: software-pipelined ------------------------------
+// The same products as sdpa_bwd_kv_dma, reordered so the matrix cores never wait on the softmax.
+// A 32-query half goes through two phases of 16 MFMAs each:
+//   X: S and dP of the *next* half (S with Q rows, dP with dO rows, alternating: two independent
+//      accumulation chains), while the VALU turns the current half's S and dP into P and dS;
+//   Y: dV^T += dO^T P and dK^T += Q^T dS of the current half (transposing reads).
+// Every slot (one MFMA plus its share of LDS reads and VALU) is fenced with sched_barrier and its
+// VALU results pinned by an empty asm, so the interleave survives both the IR optimizer (which
+// would otherwise sink the softmax down to its first use) and the scheduler. The X phase of a
+// tile's second half reads the *next* tile's rows, so tiles are triple-buffered: tile t is read,
+// t + 1 is resident, t + 2 is in flight; the loop is unrolled by three so every buffer is a
+// separate __shared__ array at a fixed address (the copy into the idle buffer provably never
+// aliases a read). Causal tiles after the first two are whole, and rows past t_q (a ragged last
+// tile, and up to two padding tiles that round the loop to whole triples) arrive as zeros with
+// zero statistics: P = 1 there but dS = 0 and dO = 0, so they add nothing. Without a key mask no
+// tile but the two diagonal ones is masked; masked calls keep sdpa_bwd_kv_dma.
+// Measured on the MI355X at 128 heads x 4096 rows, causal (the C4 step): 1.144 ms against 1.273
+// for sdpa_bwd_kv_dma, identical results; a probe of this pass with its VALU and LDS reads
+// removed runs at 1350 TFLOP/s (the MFMAs alone at 2100), and one wave per SIMD hides only a few
+// VALU instructions per MFMA of its own, which is what bounds both kernels.
+
+// the wave's 32 rows x 128 dims of an accumulator set (lane n = row, items = dims, the layout
+// store_transposed takes) to global rows [row0, row0 + 32) of a (rows x 128) matrix through an
+// LDS stage of 32 rows padded to 272 bytes: 16 8-byte LDS writes per lane, then 8 16-byte global
+// stores per lane covering 4 whole rows each. store_transposed's 8-byte stores touch 32 rows per
+// instruction; staged, the dK/dV pass above took 1.143 ms against 1.194.
+template <typename T>
+__device__ __forceinline__ void store_staged(u16* base, const f32x16* acc, int row0, int rows, float mul, u16* stage) {
+  const int lane = threadIdx.x & 63, h = lane >> 5, n = lane & 31;
+  constexpr int RS = 136;  // padded row stride, elements
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const u16x4 o = {T::pack(acc[dt][4 * g] * mul), T::pack(acc[dt][4 * g + 1] * mul), T::pack(acc[dt][4 * g + 2] * mul),
+                       T::pack(acc[dt][4 * g + 3] * mul)};
+      *(u16x4*)(stage + n * RS + dt * 32 + 8 * g + 4 * h) = o;
+    }
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int r = 4 * j + (lane >> 4), c = lane & 15;
+    const u16x8 v = *(const u16x8*)(stage + r * RS + c * 8);
+    if (row0 + r < rows) *(u16x8*)(base + (int64_t)(row0 + r) * 128 + c * 8) = v;
+  }
+}
+
+template <typename T, bool CAUSAL>
+__global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_piped(const u16* __restrict__ q, const u16* __restrict__ k,
+                                                                const u16* __restrict__ v, const u16* __restrict__ dout,
+                                                                const float* __restrict__ lse,
+                                                                const float* __restrict__ delta, u16* __restrict__ dk,
+                                                                u16* __restrict__ dv, int64_t batch, int t_q, int t_k,
+                                                                float scale) {
+  constexpr int D = 128, ROWS = 128;
+  __shared__ __attribute__((aligned(1024))) u16 Q0[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 Q1[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 Q2[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 O0[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 O1[TILE * D];
+  __shared__ __attribute__((aligned(1024))) u16 O2[TILE * D];
+  __shared__ __attribute__((aligned(16))) float L0[TILE], L1[TILE], L2[TILE], D0[TILE], D1[TILE], D2[TILE];
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
+  int64_t b, kb;  // causal: the first keys are seen by the most queries
+  head_and_block(batch, (t_k + ROWS - 1) / ROWS, b, kb);
+  const int k0 = (int)kb * ROWS, wk0 = k0 + wave * 32, key = wk0 + n;
+  const Rows krows(k + b * (int64_t)t_k * D, t_k, D), vrows(v + b * (int64_t)t_k * D, t_k, D);
+  const DmaTile128 qd(q + b * (int64_t)t_q * D, t_q, wave, lane), od(dout + b * (int64_t)t_q * D, t_q, wave, lane);
+  const SwzReads128 ad(lane);
+  const float c2 = scale * LOG2E;
+
+  u16x8 kf[8], vf[8];
+  f32x16 gk[4], gv[4];
+#pragma unroll
+  for (int ds = 0; ds < 8; ds++) {
+    kf[ds] = krows.load8(key * D + ds * 16 + 8 * h);
+    vf[ds] = vrows.load8(key * D + ds * 16 + 8 * h);
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++) {
+    gk[dt] = zero16();
+    gv[dt] = zero16();
+  }
+  const int qstart = CAUSAL ? k0 : 0;  // a causal key is seen by queries at or after it
+  const int ntiles = qstart < t_q ? (t_q - qstart + TILE - 1) / TILE : 0;
+  if (ntiles == 0) {
+    store_transposed<T, D>(dk + b * (int64_t)t_k * D, gk, key, t_k, 1.f);
+    store_transposed<T, D>(dv + b * (int64_t)t_k * D, gv, key, t_k, 1.f);
+    return;
+  }
+
+  // a tile's statistics, loaded by every wave (the same values, so no branch splits the loop
+  // body) with the tile's copy and stored into LDS once the copy is waited for; entries past t_q
+  // read as zeros through the buffer resources
+  const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc((void*)(lse + b * (int64_t)t_q), (short)0, t_q * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc((void*)(delta + b * (int64_t)t_q), (short)0, t_q * 4, 0x00020000);
+  float next_l = 0.f, next_d = 0.f;
+  auto stats_load = [&](int r0) __attribute__((always_inline)) {
+    next_l = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lrs, (r0 + lane) * 4, 0, 0));
+    next_d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(drs, (r0 + lane) * 4, 0, 0));
+  };
+  auto stats_store = [&](float* L, float* Dl) __attribute__((always_inline)) {
+    L[lane] = next_l * LOG2E;
+    Dl[lane] = next_d * scale;
+  };
+
+  f32x16 sA, dA, sB, dB;  // S and dP of a tile's first (A) and second (B) half
+  u16x8 xr[4], yr[4];     // operand rings of the X and Y phases, 3 reads ahead
+  f32x4 l4[4], d4[4];     // the statistics of the half an X phase's VALU works on
+  u16x8 pb[2], gb[2];     // that half's P and dS, packed for the Y phase
+
+  // X-phase MFMA i: S (even, Q rows) or dP (odd, dO rows) for ds = i / 2
+  auto xrow = [&](const u16* Qb, const u16* Ob, int sub, int i) __attribute__((always_inline)) {
+    return (i & 1) ? ad.rows(Ob, sub, i >> 1) : ad.rows(Qb, sub, i >> 1);
+  };
+  // Y-phase MFMA i: dV (even, dO^T) or dK (odd, Q^T) for 16-query chunk c = i / 8, dims 32 dt
+  auto ytr = [&](const u16* Qb, const u16* Ob, int sub, int i) __attribute__((always_inline)) {
+    const int c = i >> 3, dt = (i >> 1) & 3;
+    return (i & 1) ? ad.transposed(Qb, sub * 32 + 16 * c, dt) : ad.transposed(Ob, sub * 32 + 16 * c, dt);
+  };
+  auto stats_read = [&](const float* Lb, const float* Db, int sub, int g) __attribute__((always_inline)) {
+    l4[g] = *(const f32x4*)(Lb + sub * 32 + 8 * g + 4 * h);
+    d4[g] = *(const f32x4*)(Db + sub * 32 + 8 * g + 4 * h);
+  };
+  // X phase: MFMAs into (s, dp) for half xsub of (Qx, Ox) (their first 3 rows already read);
+  // VALU: P and dS of (ps, pd), half vsub of the tile at query r0, into pb, gb; its last slots
+  // read the first 3 operands of the Y phase that follows (half ysub of Qy, Oy)
+  auto xphase = [&](auto edge, f32x16& s, f32x16& dp, const u16* Qx, const u16* Ox, int xsub, f32x16& ps, f32x16& pd,
+                    int r0, int vsub, const u16* Qy, const u16* Oy, int ysub) __attribute__((always_inline)) {
+    constexpr bool EDGE = decltype(edge)::value;
+    s = zero16();
+    dp = zero16();
+    unsigned pk[8], gk2[8];
+    float pv = 0.f, gv2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      if (i + 3 < 16) xr[(i + 3) % 4] = xrow(Qx, Ox, xsub, i + 3);
+      if (i >= 13) yr[i - 13] = ytr(Qy, Oy, ysub, i - 13);
+      if (i & 1)
+        dp = T::mfma32(xr[i % 4], vf[i >> 1], dp);
+      else
+        s = T::mfma32(xr[i % 4], kf[i >> 1], s);
+      float p = fast_exp2(fmaf(ps[i], c2, -l4[i >> 2][i & 3]));
+      if (EDGE) {
+        const int qq = r0 + vsub * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        bool hide = (qq >= t_q) | (key >= t_k);
+        if (CAUSAL) hide |= qq < key;
+        p = hide ? 0.f : p;
+      }
+      const float g = p * fmaf(pd[i], scale, -d4[i >> 2][i & 3]);
+      if (i & 1) {
+        pk[i >> 1] = T::pack2(pv, p);
+        gk2[i >> 1] = T::pack2(gv2, g);
+        asm volatile("" : "+v"(pk[i >> 1]), "+v"(gk2[i >> 1]));
+      } else {
+        pv = p;
+        gv2 = g;
+        asm volatile("" : "+v"(pv), "+v"(gv2));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const u32x4 wp = {pk[4 * c], pk[4 * c + 1], pk[4 * c + 2], pk[4 * c + 3]};
+      const u32x4 wg = {gk2[4 * c], gk2[4 * c + 1], gk2[4 * c + 2], gk2[4 * c + 3]};
+      pb[c] = __builtin_bit_cast(u16x8, wp);
+      gb[c] = __builtin_bit_cast(u16x8, wg);
+    }
+  };
+  // Y phase: dV/dK MFMAs of half ysub of (Qy, Oy); its first slots read the statistics of the next
+  // X phase's VALU half (Ls, Ds, half ssub), its last slots that X phase's first rows (Qx, Ox, xsub)
+  auto yphase = [&](const u16* Qy, const u16* Oy, int ysub, const float* Ls, const float* Ds, int ssub, const u16* Qx,
+                    const u16* Ox, int xsub) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      if (i + 3 < 16) yr[(i + 3) % 4] = ytr(Qy, Oy, ysub, i + 3);
+      if (i < 4) stats_read(Ls, Ds, ssub, i);
+      if (i >= 13) xr[i - 13] = xrow(Qx, Ox, xsub, i - 13);
+      const int c = i >> 3, dt = (i >> 1) & 3;
+      if (i & 1)
+        gk[dt] = T::mfma32(yr[i % 4], gb[c], gk[dt]);
+      else
+        gv[dt] = T::mfma32(yr[i % 4], pb[c], gv[dt]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // prologue: tile 0 resident with its statistics, tile 1 in flight, S and dP of tile 0's first half
+  qd.copy(Q0, qstart, wave);
+  od.copy(O0, qstart, wave);
+  stats_load(qstart);
+  __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
+  stats_store(L0, D0);
+  qd.copy(Q1, qstart + TILE, wave);
+  od.copy(O1, qstart + TILE, wave);
+  stats_load(qstart + TILE);
+  __syncthreads();
+  sA = zero16();
+  dA = zero16();
+#pragma unroll
+  for (int i = 0; i < 3; i++) xr[i] = xrow(Q0, O0, 0, i);
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    if (i + 3 < 16) xr[(i + 3) % 4] = xrow(Q0, O0, 0, i + 3);
+    if (i < 4) stats_read(L0, D0, 0, i);
+    if (i & 1)
+      dA = T::mfma32(xr[i % 4], vf[i >> 1], dA);
+    else
+      sA = T::mfma32(xr[i % 4], kf[i >> 1], sA);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int i = 0; i < 3; i++) xr[i] = xrow(Q0, O0, 1, i);
+
+  // tile t in (Qc, Oc, Lc, Dc); tile t + 1 arriving in (Qn, On), its statistics in registers;
+  // (Qf, Of) free for tile t + 2 once every wave passes this step's barrier
+  auto step = [&](auto edge, int t, const u16* Qc, const u16* Oc, const float* Lc, const float* Dc, const u16* Qn,
+                  const u16* On, float* Ln, float* Dn, u16* Qf, u16* Of) __attribute__((always_inline)) {
+    const int r0 = qstart + t * TILE;
+    xphase(edge, sB, dB, Qc, Oc, 1, sA, dA, r0, 0, Qc, Oc, 0);  // S/dP of half 1, P/dS of half 0
+    __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
+    stats_store(Ln, Dn);
+    __syncthreads();
+    qd.copy(Qf, r0 + 2 * TILE, wave);
+    od.copy(Of, r0 + 2 * TILE, wave);
+    stats_load(r0 + 2 * TILE);
+    yphase(Qc, Oc, 0, Lc, Dc, 1, Qn, On, 0);                     // dV/dK of half 0
+    xphase(edge, sA, dA, Qn, On, 0, sB, dB, r0, 1, Qc, Oc, 1);  // S/dP of the next tile's half 0, P/dS of half 1
+    yphase(Qc, Oc, 1, Ln, Dn, 0, Qn, On, 1);                     // dV/dK of half 1
+  };
+  constexpr std::true_type masked{};
+  constexpr std::false_type whole{};
+  if (CAUSAL) {
+    step(masked, 0, Q0, O0, L0, D0, Q1, O1, L1, D1, Q2, O2);
+    if (ntiles > 1) step(masked, 1, Q1, O1, L1, D1, Q2, O2, L2, D2, Q0, O0);
+    for (int t = 2; t < ntiles; t += 3) {
+      step(whole, t, Q2, O2, L2, D2, Q0, O0, L0, D0, Q1, O1);
+      step(whole, t + 1, Q0, O0, L0, D0, Q1, O1, L1, D1, Q2, O2);
+      step(whole, t + 2, Q1, O1, L1, D1, Q2, O2, L2, D2, Q0, O0);
+    }
+  } else {
+    for (int t = 0; t < ntiles; t += 3) {
+      step(whole, t, Q0, O0, L0, D0, Q1, O1, L1, D1, Q2, O2);
+      step(whole, t + 1, Q1, O1, L1, D1, Q2, O2, L2, D2, Q0, O0);
+      step(whole, t + 2, Q2, O2, L2, D2, Q0, O0, L0, D0, Q1, O1);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(WAIT_VMEM);  // the copies issued for tiles past the end
+  __syncthreads();                        // every wave is done with the tile buffers
+  u16* stage = wave == 0 ? Q0 : wave == 1 ? Q1 : wave == 2 ? O0 : O1;
+  store_staged<T>(dk + b * (int64_t)t_k * D, gk, wk0, t_k, 1.f, stage);
+  store_staged<T>(dv + b * (int64_t)t_k * D, gv, wk0, t_k, 1.f, stage);
+}
+
 // ---- forward at D = 128: streamed K and V tiles copied straight into LDS ------------------------
 // The same swizzled tiles and LDS DMA as the dK/dV pass above: K is read as row operands of
 // S^T = K Q^T, V through the transposing reads of O^T += V^T P^T. Tiles that need masking (a
@@ -1084,7 +1338,9 @@ __global__ __launch_bounds__(THREADS, 2) void sdpa_fwd_dma(const u16* __restrict
   run(std::false_type{}, 0, open);
   run(std::true_type{}, open, ntiles);
   const float total = pair_sum(l);
-  store_transposed<T, D>(out + b * (int64_t)t_q * D, acc, row, t_q, 1.f / total);
+  // the tile buffers are free: the last step waited for its copy and passed the barrier
+  u16* stage = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? V0 : V1;
+  store_staged<T>(out + b * (int64_t)t_q * D, acc, q0 + wave * 32, t_q, 1.f / total, stage);
   if (h == 0 && row < t_q) lse[b * (int64_t)t_q + row] = m * scale + logf(total);
 }
 
@@ -1216,7 +1472,8 @@ __global__ __launch_bounds__(THREADS, 2) void sdpa_bwd_q_dma(const u16* __restri
   if (open > ntiles) open = ntiles;
   run(std::false_type{}, 0, open);
   run(std::true_type{}, open, ntiles);
-  store_transposed<T, D>(dq + b * (int64_t)t_q * D, acc, row, t_q, 1.f);
+  u16* stage = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? V0 : V1;  // free after the last barrier
+  store_staged<T>(dq + b * (int64_t)t_q * D, acc, q0 + wave * 32, t_q, 1.f, stage);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1256,6 +1513,10 @@ int launch_nt(const SdpaArgs& a) {
     hipLaunchKernelGGL((sdpa_bwd_q_mfma<T, D, NT, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q,
                        (const u16*)a.k, (const u16*)a.v, (const u16*)a.dout, (const float*)a.lse, (const float*)a.delta,
                        mask, (u16*)a.out0, a.batch, (int)a.t_q, (int)a.t_k, scale);
+  } else if constexpr (D == 128 && !MASK) {
+    hipLaunchKernelGGL((sdpa_bwd_kv_piped<T, CAUSAL>), grid, block, 0, a.stream, (const u16*)a.q, (const u16*)a.k,
+                       (const u16*)a.v, (const u16*)a.dout, (const float*)a.lse, (const float*)a.delta, (u16*)a.out0,
+                       (u16*)a.out1, a.batch, (int)a.t_q, (int)a.t_k, scale);
   } else if constexpr (D == 128) {
     hipLaunchKernelGGL((sdpa_bwd_kv_dma<T, CAUSAL, MASK>), grid, block, 0, a.stream, (const u16*)a.q, (const u16*)a.k,
                        (const u16*)a.v, (const u16*)a.dout, (const float*)a.lse, (const float*)a.delta, mask,

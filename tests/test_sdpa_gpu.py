@@ -136,6 +136,10 @@ MFMA_CASES = {
     "d64_ragged": ((2, 2, 200, 64), (2, 2, 200, 64), (2, 2, 200, 64)),
     "d128_two_blocks": ((1, 2, 256, 128), (1, 2, 256, 128), (1, 2, 256, 128)),
     "d128_ragged": ((2, 1, 333, 128), (2, 1, 333, 128), (2, 1, 333, 128)),
+    # the pipelined dK/dV pass: 10 and 13 query tiles per key block, loops of whole triples
+    # with padding tiles, a ragged last tile past the diagonal
+    "d128_long": ((1, 2, 640, 128), (1, 2, 640, 128), (1, 2, 640, 128)),
+    "d128_long_ragged": ((1, 1, 801, 128), (1, 1, 801, 128), (1, 1, 801, 128)),
 }
 
 
@@ -148,6 +152,11 @@ def test_mfma_family_matches_the_oracle(hipdev, case, causal, dtype_name):
 
 def test_mfma_family_rectangular_keys(hipdev):
     check_case(hipdev, 6, ((3, 70, 64), (3, 190, 64), (3, 190, 64)), False, "bfloat16")
+
+
+@pytest.mark.parametrize("t_q,t_k", [(70, 390), (390, 70)])
+def test_mfma_family_rectangular_d128(hipdev, t_q, t_k):
+    check_case(hipdev, 8, ((2, t_q, 128), (2, t_k, 128), (2, t_k, 128)), False, "bfloat16")
 
 
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
