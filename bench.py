@@ -122,7 +122,7 @@ def _short_kernel(name: str) -> str:
     """A template kernel's rocprofv3 name, shortened: `sdpa_bwd_kv_dma<BF16,true,false>`."""
     import re
 
-    m = re.search(r"(\w+_(?:mfma|dma|rows))<([^()]*)>", name)
+    m = re.search(r"(\w+_(?:mfma|dma|rows|piped))<([^()]*)>", name)
     if m:
         return f"{m.group(1)}<{m.group(2).replace('limn::', '').replace(' ', '')}>"
     return name.split("(")[0].replace("void ", "")
@@ -805,7 +805,7 @@ def main() -> int:
     KERNEL_SYMBOL = {
         "sdpa": "sdpa_fwd_dma<BF16,true,false>",
         "sdpa_bwd_q": "sdpa_bwd_q_dma<BF16,true,false>",
-        "sdpa_bwd_kv": "sdpa_bwd_kv_dma<BF16,true,false>",
+        "sdpa_bwd_kv": "sdpa_bwd_kv_piped<BF16,true>",
     }
     dom = int(np.argmax(per))
     achieved = kernel_flops[names[dom]] / (per[dom] * 1e-3)

@@ -236,3 +236,23 @@ def test_merged_kernel_binds_each_members_buffers():
     source, grid = emit.merged_source("merged", nests, plans, runs[0])
     assert grid == sum(plans[c].launches[0].grid for c in runs[0])
     assert "s0_in0" in source and "s1_out" in source and source.count("const i64 bid_") == 2
+
+
+def test_a_large_sink_streams_its_stores():
+    """An output of STREAM_BYTES or more that no later nest reads is written non-temporally; a
+    read-again output and a small sink keep plain stores."""
+    n = 4096  # 4096 x 4096 float32 = 64 MiB
+    x = Tensor(np.zeros((n, n), np.float32))
+    doubled = x * 2.0
+    out = (doubled + 1.0).relu()
+    small = (Tensor(np.zeros((8, 8), np.float32)) * 3.0)
+    nests, kept = lowered([out, doubled, small])
+    streamed = emit.streamed_outputs(nests, kept, set())
+    names = {nests[k].kernel.target for k in streamed}
+    assert names == {realized(out.node)}
+    prog = emit.plan_program(nests, kept, set())
+    sources = {nests[k].kernel.target: prog.plans[k].source for k in range(len(nests))}
+    assert "__builtin_nontemporal_store" in sources[realized(out.node)]
+    assert "__builtin_nontemporal_store" not in sources[realized(doubled.node)]
+    assert "__builtin_nontemporal_store" not in sources[realized(small.node)]
+    assert emit.streamed_outputs(nests, None, None) == set()
