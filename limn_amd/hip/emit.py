@@ -126,17 +126,25 @@ def store_expr(dtype: DType, value: str) -> str:
 
 
 def arith(op: Op, srcs: tuple[str, ...], dtype: DType) -> str:
+    """One ARITH instruction as a C expression at the value type of `dtype`. A half-width node
+    (bf16, f16) is computed in float and rounded to 8 or 11 significand bits, so its EXP and RECIP
+    take the hardware's approximations (v_exp_f32 on x log2 e, v_rcp_f32: within 2 ulp of float,
+    far under that rounding) instead of the correctly rounded library forms, which cost ten or more
+    instructions each: a composed tanh GELU over a (16384, 2048) bf16 activation is bound by them."""
     t = VALUE_T[dtype]
     wide = dtype == float64
+    half = dtype in (bfloat16, float16)
     if op is Op.NEG:
         return f"({t})(-{srcs[0]})"
     if op is Op.EXP:
-        return f"{'exp' if wide else 'expf'}({srcs[0]})"
+        return f"__expf({srcs[0]})" if half else f"{'exp' if wide else 'expf'}({srcs[0]})"
     if op is Op.LOG:
         return f"{'log' if wide else 'logf'}({srcs[0]})"
     if op is Op.SQRT:
         return f"{'sqrt' if wide else 'sqrtf'}({srcs[0]})"
     if op is Op.RECIP:
+        if half:
+            return f"__builtin_amdgcn_rcpf({srcs[0]})"
         return f"({'1.0' if wide else '1.0f'} / {srcs[0]})"
     if op is Op.ADD:
         return f"fadd(({t}){srcs[0]}, ({t}){srcs[1]})" if dtype in INTS else f"({srcs[0]} + {srcs[1]})"
