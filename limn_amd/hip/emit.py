@@ -1013,6 +1013,7 @@ def fold_parts(name: str, shape: NestShape, acc_t: str, out_dtype: DType, out_re
 
 COLUMN_TILE = 64  # cells per workgroup of a column reduce: one wave's lanes, one coalesced row piece
 COLUMN_BLOCKS = 2048  # workgroups a column reduce aims for (8 per CU): tiles x row parts
+COLUMN_ROWS = 16  # the fewest rows a wave of a column reduce folds
 
 
 def plan_columns(nest: LoopNest, shape: NestShape, bufs: Buffers, cells: int, R: int) -> Planned:
@@ -1035,8 +1036,8 @@ def plan_columns(nest: LoopNest, shape: NestShape, bufs: Buffers, cells: int, R:
     vec = _vec_width(shape, bufs, along, along_extent)
     per_tile = COLUMN_TILE * vec
     tiles = -(-cells // per_tile)
-    # parts enough to fill the machine, each wave reading at least 16 rows of its part
-    parts = max(1, min(-(-COLUMN_BLOCKS // tiles), R // (16 * waves)))
+    # parts enough to fill the machine, each wave reading at least COLUMN_ROWS rows of its part
+    parts = max(1, min(-(-COLUMN_BLOCKS // tiles), R // (COLUMN_ROWS * waves)))
     per_part = -(-R // parts)
     out_ref = f"out[{render_index(shape.out_index, wide)}]"
     base_vars = shape.outer[:-1] + [(along + "_b", along_extent // vec)]
