@@ -169,6 +169,11 @@ class Buffers:
     wide_index: bool
     inline: dict[str, "Inlined"] = field(default_factory=dict)
     extra: list[str] = field(default_factory=list)
+    # a row program's per-row values: a load of this buffer reads the named variable (the value
+    # an earlier member of the program stored for this row) rounded as its store rounded it
+    rowvals: dict[str, tuple[str, DType]] = field(default_factory=dict)
+    # a row program's cached row: the load defining this value reads the named register instead
+    cached: dict[str, str] = field(default_factory=dict)
 
 
 @dataclass(frozen=True)
@@ -208,6 +213,11 @@ def value_line(instr: Instr, bufs: Buffers) -> str:
         if valid.bounds:
             return f"const {t} {instr.dest} = ({valid.render()}) ? {lit} : ({t})0;"
         return f"const {t} {instr.dest} = {lit};"
+    if op is Opcode.LOAD and instr.dest in bufs.cached:
+        return f"const {t} {instr.dest} = ({t}){bufs.cached[instr.dest]};"
+    if op is Opcode.LOAD and instr.arg[0] in bufs.rowvals:
+        var, dt = bufs.rowvals[instr.arg[0]]
+        return f"const {t} {instr.dest} = ({t}){load_expr(dt, store_expr(dt, var))};"
     if op is Opcode.LOAD and instr.arg[0] in bufs.inline:
         return inline_load(instr, bufs.inline[instr.arg[0]], bufs)
     if op is Opcode.LOAD:
@@ -499,7 +509,7 @@ def run_loads(nest: LoopNest, body: list[Instr], bufs: Buffers, var: str, vec: i
         if instr.opcode is not Opcode.LOAD:
             continue
         buf, index, valid = instr.arg
-        if buf in bufs.inline or any(b[0] == var for b in valid.bounds):
+        if buf in bufs.inline or buf in bufs.rowvals or instr.dest in bufs.cached or any(b[0] == var for b in valid.bounds):
             continue
         if dict(index.terms).get(var) != 1 or sizes.get(buf, 0) < vec:
             continue
@@ -1315,7 +1325,7 @@ MERGE_MEMBERS = 16  # the most nests in one merged launch
 
 
 def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set | None, inlined: "InlineSet",
-               pairs: dict[int, int]) -> list[list[int]]:
+               pairs: dict[int, int], taken: set[int] = frozenset()) -> list[list[int]]:
     """Groups of small elementwise nests that can share one launch, made at the place of the
     group's last member. A member joins when it reads no other member's output (directly or
     through an inlined producer); a nest between members that is not one may stay between them
@@ -1324,8 +1334,8 @@ def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set |
     between nests. Each member is at most MERGE_GRID workgroups, a group at most MERGE_MEMBERS
     nests and MERGE_GROUP_GRID workgroups. An optimizer step gives such groups across parameters (each parameter's moments, then
     the parameter from the new moments, with the next parameter's gradient reduce between):
-    launches of a few microseconds each for the small parameters. `custom_inputs` None merges
-    nothing."""
+    launches of a few microseconds each for the small parameters. Nests in `taken` (members of
+    row programs) never join. `custom_inputs` None merges nothing."""
     if custom_inputs is None:
         return []
     fused = set(pairs) | set(pairs.values())
@@ -1352,6 +1362,7 @@ def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set |
         ok = (
             "body" in plan.notes
             and c not in fused
+            and c not in taken
             and len(plan.launches) == 1
             and plan.launches[0].grid <= MERGE_GRID
             and nest.kernel.target not in custom_inputs
@@ -1391,6 +1402,391 @@ def merged_source(name: str, nests: list[LoopNest], plans: list[Planned], run: l
     segments.append("  }")
     source = f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}({", ".join(params)}) {{\n' + "\n".join(segments) + "\n}"
     return source, offset
+
+
+
+# ---- row programs ---------------------------------------------------------------------------
+# A softmax or a LayerNorm reaches the device as a chain of nests over the same rows: row
+# reductions (a max, a sum, a sum of squares) each writing one value per row, and elementwise
+# nests over the rows' cells reading those values. Launched one by one, each reduction streams
+# the whole input again, and each launch of a few microseconds is paid in full on short rows.
+# A row program runs such a chain as one kernel: a workgroup (long rows) or a wave (rows of up to
+# 64 vector chunks per lane group) takes a row and runs every member on it in plan order, each
+# reduction's total kept in registers for the later members (their loads of it read the
+# register, rounded as the store rounds) and stored as well. Each member's code is the code its
+# own kernel would run for that row (the same strided loop, vector width and fold order), so the
+# results are the same bits; the input row is re-read from the caches rather than from HBM.
+
+@dataclass
+class RowMember:
+    """A nest as a member of a row program: `kind` "reduce" (one value per row, folded over the
+    row's cells), "cells" (an elementwise nest over the row's cells) or "scalar" (an elementwise
+    nest with one cell per row); its row loop variables, its cell variable and extent (None for
+    "scalar"), and for a reduce the lanes its own kernel gives a row (THREADS or 64) and its vector
+    width."""
+
+    kind: str
+    rows: tuple[int, ...]
+    row_vars: list[tuple[str, int]]
+    col: tuple[str, int] | None
+    group: int | None
+    vec: int
+    shape: NestShape
+
+
+def _row_strides(row_vars: list[tuple[str, int]]) -> dict[str, int]:
+    strides, step = {}, 1
+    for var, extent in reversed(row_vars):
+        if extent > 1:
+            strides[var] = step
+            step *= extent
+    return strides
+
+
+def row_flat(index: Index, row_vars: list[tuple[str, int]], scale: int = 1) -> bool:
+    """Whether `index` is the row-major position of the row (times `scale`) in `row_vars`: each
+    variable of extent > 1 at its row-major stride, no constant, no other variable."""
+    if index.const:
+        return False
+    strides = _row_strides(row_vars)
+    ones = {v for v, e in row_vars if e == 1}
+    seen = set()
+    for var, coeff in index.terms:
+        if var in strides:
+            if coeff != strides[var] * scale:
+                return False
+            seen.add(var)
+        elif var not in ones:
+            return False
+    return seen == set(strides)
+
+
+def row_member(nest: LoopNest, plan: Planned) -> RowMember | None:
+    """How a nest would run inside a row program, or None when it cannot."""
+    if plan.contraction is not None or len(plan.launches) != 1 or "params" not in plan.notes:
+        return None
+    target = nest.kernel.target
+    if target.dtype not in (float32, bfloat16, float16):
+        return None
+    shape = read_nest(nest)
+    if shape.fold is not None:
+        group = plan.notes.get("group")
+        if group not in (THREADS, 64) or plan.notes.get("columns") or len(shape.inner) != 1:
+            return None
+        if shape.reduce_dtype not in (float32, bfloat16, float16):
+            return None
+        col = shape.inner[0]
+        vec = plan.notes.get("vec", 1)
+        if stride_one_var(nest, shape) != col[0] or (group == 64 and col[1] // vec < 64):
+            return None
+        if not row_flat(shape.out_index, shape.outer):
+            return None
+        rows = tuple(e for _, e in shape.outer if e > 1)
+        return RowMember("reduce", rows, list(shape.outer), col, group, vec, shape)
+    if not plan.notes.get("elementwise") or shape.write is None or shape.write.opcode is not Opcode.STORE:
+        return None
+    out_index = shape.write.arg[1]
+    if shape.outer and shape.outer[-1][1] > 1 and dict(out_index.terms).get(shape.outer[-1][0]) == 1:
+        col = shape.outer[-1]
+        rest = Index(out_index.const, tuple((v, c) for v, c in out_index.terms if v != col[0]))
+        if not row_flat(rest, shape.outer[:-1], col[1]):
+            return None
+        rows = tuple(e for _, e in shape.outer[:-1] if e > 1)
+        return RowMember("cells", rows, list(shape.outer[:-1]), col, None, 1, shape)
+    if not row_flat(out_index, shape.outer):
+        return None
+    rows = tuple(e for _, e in shape.outer if e > 1)
+    return RowMember("scalar", rows, list(shape.outer), None, None, 1, shape)
+
+
+def _loads(body) -> list[Instr]:
+    return [i for i in body if i.opcode in (Opcode.LOAD, Opcode.GATHER)]
+
+
+def _reads_rows_only(nest: LoopNest, member: RowMember, made: set, inlined: "InlineSet") -> bool:
+    """Whether every read of a value `made` earlier in the program, by the nest or by a producer
+    it evaluates in place, is a plain load of this row's value."""
+    producers = {inlined.nests[j].kernel.target: j for j in inlined.reached(nest)}
+    # producers whose value depends on something made in the program (directly or through another)
+    tainted: set = set()
+    changed = True
+    while changed:
+        changed = False
+        for target, j in producers.items():
+            if target in tainted:
+                continue
+            if any(n in made or n in tainted for n in inlined.nests[j].kernel.inputs):
+                tainted.add(target)
+                changed = True
+    needs = made | tainted
+
+    def ok(body, inputs, row_vars) -> bool:
+        for instr in _loads(body):
+            node = inputs[int(instr.arg[0][2:])] if instr.arg[0].startswith("in") else None
+            if node is None or node not in needs:
+                continue
+            if instr.opcode is Opcode.GATHER or instr.arg[2].bounds or not row_flat(instr.arg[1], row_vars):
+                return False
+        return True
+
+    if not ok(member.shape.body, nest.kernel.inputs, member.row_vars):
+        return False
+    for target, j in producers.items():
+        if target not in tainted:
+            continue
+        pn = inlined.nests[j]
+        space = [(f"i{d}", e) for d, e in enumerate(pn.kernel.target.shape)]
+        if not ok(read_nest(pn).body, pn.kernel.inputs, space):
+            return False
+    return True
+
+
+def row_chains(nests: list[LoopNest], plans: list[Planned], custom_inputs: set | None, inlined: "InlineSet",
+               pairs: dict[int, int]) -> list[list[int]]:
+    """Runs of nests to run as row programs: consecutive in the plan (nests between members stay,
+    and run before the program, unless they read a member's output, which ends the run), over
+    the same rows and row length, reductions of one kind (a workgroup or a wave per row), every
+    read of a member's output a plain load of the same row. A run needs a reduction and two
+    members. No member's output may be a CUSTOM input; `custom_inputs` None builds none."""
+    if custom_inputs is None:
+        return []
+    fused = set(pairs) | set(pairs.values())
+
+    def reads(c: int) -> set:
+        nodes = set(nests[c].kernel.inputs)
+        for j in inlined.reached(nests[c]):
+            nodes |= set(nests[j].kernel.inputs)
+        return nodes
+
+    chains: list[list[int]] = []
+    run: list[int] = []
+    made: set = set()
+    key: dict = {}
+
+    def close() -> None:
+        kinds = [row_member(nests[c], plans[c]).kind for c in run]
+        if len(run) > 1 and "reduce" in kinds:
+            chains.append(list(run))
+        run.clear()
+        made.clear()
+        key.clear()
+
+    for c, nest in enumerate(nests):
+        if c in inlined.producers:
+            continue
+        m = None
+        if c not in fused and plans[c].launches and nest.kernel.target not in custom_inputs:
+            m = row_member(nest, plans[c])
+        if m is not None and run:
+            fits = m.rows == key["rows"] and (m.col is None or key["cols"] in (None, m.col[1]))
+            fits = fits and (m.group is None or key["group"] in (None, m.group))
+            if fits and _reads_rows_only(nest, m, made, inlined) and all(
+                    row_member(nests[p], plans[p]).kind != "cells" for p in run if nests[p].kernel.target in reads(c)):
+                run.append(c)
+                made.add(nest.kernel.target)
+                key["cols"] = key["cols"] if m.col is None else m.col[1]
+                key["group"] = key["group"] if m.group is None else m.group
+                continue
+        if run and (m is not None or reads(c) & made):
+            close()
+        if m is not None:
+            run.append(c)
+            made.add(nest.kernel.target)
+            key.update(rows=m.rows, cols=None if m.col is None else m.col[1], group=m.group)
+    close()
+    return chains
+
+
+# A row program keeps the row of an input that two or more members read at (row, cell) in
+# registers, up to this many values a thread: the row comes from HBM once and every later pass
+# over it reads the registers. Re-read from memory, the passes of an 8192-float row softmax then
+# LayerNorm (32 KB a row, thousands of rows in flight) missed the L2 and ran at 2.5 TB/s of
+# algorithmic bytes; the row is 32 values a thread of a 256-thread workgroup.
+ROW_CACHE_VALUES = 32
+
+
+def _row_read(instr: Instr, inputs: list, member: RowMember):
+    """The input node that a member's LOAD reads at the member's (row, cell), unmasked - index the
+    row's row-major position times the row length plus the cell - or None."""
+    if instr.opcode is not Opcode.LOAD or not instr.arg[0].startswith("in") or member.col is None:
+        return None
+    buf, index, valid = instr.arg
+    node = inputs[int(buf[2:])]
+    col_var, cols = member.col
+    if valid.bounds or node.dtype not in (float32, bfloat16, float16) or dict(index.terms).get(col_var) != 1:
+        return None
+    rest = Index(index.const, tuple((v, c) for v, c in index.terms if v != col_var))
+    return node if row_flat(rest, member.row_vars, cols) else None
+
+
+def row_source(name: str, nests: list[LoopNest], plans: list[Planned], run: list[int], inlined: "InlineSet",
+               streamed: set[int]) -> tuple[str, int]:
+    """One kernel for a row program (see row_chains): each member's parameters bound as its own
+    kernel's, its code for one row, in order, inside one loop over the rows. Inputs that several
+    members read along the row are loaded into registers once per row (ROW_CACHE_VALUES); the
+    members' loops then run unrolled over the same cells in the same order, so every fold adds in
+    the order of the member's own kernel."""
+    members = [(c, row_member(nests[c], plans[c])) for c in run]
+    group = next(m.group for _, m in members if m.kind == "reduce")
+    rows = math.prod(members[0][1].rows)
+    cols = next(m.col[1] for _, m in members if m.col is not None)
+    threads = THREADS if group == THREADS else 64
+    tid = "threadIdx.x" if group == THREADS else "lane_"
+    # each member's buffers and cells per thread step
+    setup = []
+    for c, m in members:
+        kernel = nests[c].kernel
+        dtypes = {f"in{k}": n.dtype for k, n in enumerate(kernel.inputs)}
+        dtypes["out"] = kernel.target.dtype
+        biggest = max([math.prod(n.shape) for n in kernel.inputs] + [math.prod(kernel.target.shape)])
+        bufs = Buffers(dtypes, wide_index=biggest >= (1 << 31) - 1)
+        if inlined.reached(nests[c]):
+            inlined.bind(nests[c], bufs)
+        vec = m.vec if m.kind == "reduce" else _vec_width(m.shape, bufs, *m.col) if m.kind == "cells" else 1
+        setup.append((bufs, vec))
+    # the cached rows: node -> (variable, vec, passes, member slots that read it)
+    readers: dict = {}
+    for s_, (c, m) in enumerate(members):
+        for instr in _loads(m.shape.body):
+            node = _row_read(instr, nests[c].kernel.inputs, m)
+            if node is not None and s_ not in readers.setdefault(node, []):
+                readers[node].append(s_)
+    cache: dict = {}
+    room = ROW_CACHE_VALUES
+    for node, slots in readers.items():
+        vec = setup[slots[0]][1]
+        same = [s_ for s_ in slots if setup[s_][1] == vec]
+        passes = -(-(cols // vec) // threads)
+        if len(same) < 2 or passes * vec > room:
+            continue
+        room -= passes * vec
+        cache[node] = (f"rc{len(cache)}_", vec, passes, same)
+    params: list[str] = []
+    lines: list[str] = []
+    values: dict = {}  # node -> (variable, stored dtype) of members with one value per row
+    if group == THREADS:
+        lines.append(f"  __shared__ float rp_fold_[{THREADS // 64}];")
+        lines.append(f"  for (i64 row_ = blockIdx.x; row_ < {rows}LL; row_ += gridDim.x) {{")
+        grid = max(1, min(rows, 1 << 20))
+    else:
+        per = THREADS // 64
+        lines.append("  const int lane_ = threadIdx.x & 63;")
+        lines.append(f"  for (i64 row_ = (i64)blockIdx.x * {per} + (threadIdx.x >> 6); row_ < {rows}LL; row_ += (i64)gridDim.x * {per}) {{")
+        grid = max(1, min(-(-rows // per), 1 << 20))
+    for node, (var, vec, passes, same) in cache.items():
+        first = same[0]
+        k = next(k for k, n in enumerate(nests[members[first][0]].kernel.inputs) if n is node)
+        st, chunks = STORE_T[node.dtype], cols // vec
+        lines.append(f"    {VALUE_T[node.dtype]} {var}[{passes}][{vec}];")
+        lines.append("#pragma unroll")
+        lines.append(f"    for (int it_ = 0; it_ < {passes}; it_++) {{")
+        lines.append(f"      const i64 c_ = {tid} + (i64)it_ * {threads};")
+        if chunks % threads:
+            lines.append(f"      if (c_ >= {chunks}LL) break;")
+        lines.append(f"      const {st}* p_ = (const {st}*)__builtin_assume_aligned(s{first}_in{k}, 16) + row_ * {cols}LL + c_ * {vec};")
+        lines.append("#pragma unroll")
+        lines.append(f"      for (int j_ = 0; j_ < {vec}; j_++) {var}[it_][j_] = {load_expr(node.dtype, 'p_[j_]')};")
+        lines.append("    }")
+
+    def cell_loop(s_: int, chunks: int, indent: str) -> tuple[list[str], bool]:
+        """The member's loop over its cell chunks: strided, or unrolled over the cached passes."""
+        c, m = members[s_]
+        bufs = setup[s_][0]
+        hits = [(node, entry) for node, entry in cache.items() if s_ in entry[3]]
+        if not hits:
+            return [f"{indent}for (i64 c_ = {tid}; c_ < {chunks}LL; c_ += {threads}) {{"], False
+        for instr in _loads(m.shape.body):
+            node = _row_read(instr, nests[c].kernel.inputs, m)
+            if node in cache and s_ in cache[node][3]:
+                bufs.cached[instr.dest] = f"{cache[node][0]}[it_][j_]"
+        passes = hits[0][1][2]
+        out = ["#pragma unroll", f"{indent}for (int it_ = 0; it_ < {passes}; it_++) {{",
+               f"{indent}  const i64 c_ = {tid} + (i64)it_ * {threads};"]
+        if chunks % threads:
+            out.append(f"{indent}  if (c_ >= {chunks}LL) break;")
+        return out, True
+
+    for s_, (c, m) in enumerate(members):
+        nest, plan, shape = nests[c], plans[c], m.shape
+        kernel = nest.kernel
+        bufs = setup[s_][0]
+        names = {f"in{k}": n for k, n in enumerate(kernel.inputs)}
+        for j, mm in inlined.extras(nest):
+            names[f"p{j}_in{mm}"] = nests[j].kernel.inputs[mm]
+        for pname, node in names.items():
+            if node in values:
+                bufs.rowvals[pname] = values[node]
+        out_dtype = kernel.target.dtype
+        wide = True
+        binds = []
+        for ctype, pname, const in plan.notes["params"]:
+            q = "const " if const else ""
+            params.append(f"{q}{ctype}* __restrict__ ALIGNED s{s_}_{pname}")
+            binds.append(f"      {q}{ctype}* __restrict__ {pname} = ({q}{ctype}*)__builtin_assume_aligned(s{s_}_{pname}, 16);")
+        var = f"rv{s_}_"
+        if m.kind != "cells":
+            lines.append(f"    float {var};")
+        lines.append(f"    {{  // {nest.name}")
+        lines += binds
+        lines += decode(m.row_vars, "row_", "      ", wide)
+        if m.kind == "reduce":
+            acc_dt = accumulate_in(shape.reduce_dtype)
+            acc_t = VALUE_T[acc_dt]
+            ident = literal(shape.identity, acc_dt)
+            inner_var, inner_extent = m.col
+            vec = m.vec
+            chunks = inner_extent // vec
+            lines.append(f"      {acc_t} acc = {ident};")
+            lines += cell_loop(s_, chunks, "      ")[0]
+            lines += decode([(inner_var + "_b", chunks)], "c_", "        ", True)
+            lines.append("#pragma unroll")
+            lines.append(f"        for (int j_ = 0; j_ < {vec}; j_++) {{")
+            lines.append(f"        const int {inner_var} = {inner_var}_b * {vec} + j_;")
+            lines += ["        " + value_line(i, bufs) for i in shape.body]
+            lines.append("        " + _fold(shape.fold, "acc", f"({acc_t}){shape.item}"))
+            lines += ["        }", "      }"]
+            lines.append(f"      acc = {'wave_fold_add' if shape.fold is Op.ADD else 'wave_fold_max'}(acc);")
+            if group == THREADS:
+                lines.append("      if ((threadIdx.x & 63) == 0) rp_fold_[threadIdx.x >> 6] = acc;")
+                lines.append("      __syncthreads();")
+                lines.append("      acc = rp_fold_[0];")
+                for w in range(1, THREADS // 64):
+                    lines.append("      " + _fold(shape.fold, "acc", f"rp_fold_[{w}]"))
+                lines.append("      __syncthreads();")
+            out_ref = f"out[{render_index(shape.out_index, wide)}]"
+            lines.append(f"      if ({tid} == 0) {out_ref} = {store_expr(out_dtype, 'acc')};")
+            lines.append(f"      {var} = (float)acc;")
+            values[kernel.target] = (var, out_dtype)
+        elif m.kind == "scalar":
+            lines += ["      " + value_line(i, bufs) for i in shape.body]
+            write = shape.write
+            lines.append(f"      if ({tid} == 0) out[{render_index(write.arg[1], wide)}] = {store_expr(out_dtype, write.srcs[0])};")
+            lines.append(f"      {var} = (float){write.srcs[0]};")
+            values[kernel.target] = (var, out_dtype)
+        else:
+            col_var, extent = m.col
+            vec = setup[s_][1]
+            write = shape.write
+            loop, _ = cell_loop(s_, extent // vec, "      ")
+            pre, runs = run_loads(nest, shape.body, bufs, col_var, vec, "        ") if vec > 1 else ([], {})
+            stream = c in streamed
+            lines += loop
+            lines.append(f"        const i64 {col_var}_b = c_;")
+            lines += pre
+            if vec > 1:
+                lines.append(f"        {STORE_T[out_dtype]}* out_p = out + (i64)({run_start(write.arg[1], col_var, vec)});")
+            lines.append("#pragma unroll")
+            lines.append(f"        for (int j_ = 0; j_ < {vec}; j_++) {{")
+            lines.append(f"        const int {col_var} = {col_var}_b * {vec} + j_;")
+            for instr in shape.body:
+                lines += ["        " + ln for ln in runs[instr.dest]] if instr.dest in runs else ["        " + value_line(instr, bufs)]
+            ref = "out_p[j_]" if vec > 1 else f"out[{render_index(write.arg[1], wide)}]"
+            lines.append("        " + store_line(ref, store_expr(out_dtype, write.srcs[0]), stream))
+            lines += ["        }", "      }"]
+        lines.append("    }")
+    lines += ["  }", "}"]
+    source = f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}({", ".join(params)}) {{\n' + "\n".join(lines)
+    return source, grid
 
 
 # Outputs of at least this many bytes that nothing later in the plan reads are written with
@@ -1451,10 +1847,12 @@ class Program:
         return "contraction" if self.plans[k].contraction is not None else "launch"
 
 
-def plan_program(nests: list[LoopNest], kept: set | None, custom_inputs: set | None) -> Program:
+def plan_program(nests: list[LoopNest], kept: set | None, custom_inputs: set | None, rows: bool = True) -> Program:
     """Plan every nest of one executor plan: contractions and their relu epilogues
     (epilogue_pairs), small broadcast producers evaluated in their readers (inline_producers),
-    groups of small independent nests sharing a launch (merge_runs). `kept` is the buffers the
+    chains of row reductions and their readers run as one row program each (row_chains; `rows`
+    False builds none), groups of small independent nests sharing a launch (merge_runs). `kept`
+    is the buffers the
     plan must keep (sinks and CUSTOM inputs) and `custom_inputs` the CUSTOM inputs alone, both
     recorded by the device's plan_of; None for either turns the optimisations that need it off.
     Touches no GPU."""
@@ -1470,15 +1868,22 @@ def plan_program(nests: list[LoopNest], kept: set | None, custom_inputs: set | N
             plans[c] = plan_nest(nest, inlined, stream=c in streamed)
     for j in inlined.producers:
         plans[j] = Planned("", [], notes={"inlined": True})
-    runs = merge_runs(nests, plans, custom_inputs, inlined, pairs)
+    chains = row_chains(nests, plans, custom_inputs, inlined, pairs) if rows else []
+    runs = merge_runs(nests, plans, custom_inputs, inlined, pairs, {c for chain in chains for c in chain})
     merged: dict[int, tuple[list[int], Launch]] = {}
     merged_sources = []
+    for chain in chains:
+        name = f"{nests[chain[0]].name}_rows_{nests[chain[-1]].name}"
+        source, grid = row_source(name, nests, plans, chain, inlined, streamed)
+        merged_sources.append(source)
+        merged[chain[-1]] = (chain, Launch(name, grid, THREADS, "merged"))
+    runs_all = runs + chains
     for run in runs:
         name = f"{nests[run[0]].name}_to_{nests[run[-1]].name}"
         source, grid = merged_source(name, nests, plans, run)
         merged_sources.append(source)
         merged[run[-1]] = (run, Launch(name, grid, THREADS, "merged"))
-    in_run = {c for run in runs for c in run}
+    in_run = {c for run in runs_all for c in run}
     names = [launch.name for k, p in enumerate(plans) if k not in in_run for launch in p.launches]
     names += [launch.name for _, launch in merged.values()]
     kept_sources = [p.source for k, p in enumerate(plans) if k not in in_run]
@@ -1492,7 +1897,8 @@ def nest_runners(dev, nests: list[LoopNest]):
     from the relu nest's runner (see epilogue_pairs); small broadcast producers run inside their
     readers (inline_producers); groups of small independent elementwise nests share one launch
     from their last member's runner (merge_runs)."""
-    prog = plan_program(nests, getattr(dev, "plan_kept", None), getattr(dev, "plan_custom_inputs", None))
+    prog = plan_program(nests, getattr(dev, "plan_kept", None), getattr(dev, "plan_custom_inputs", None),
+                        getattr(dev, "row_programs", True))
     plans, pairs, inlined, merged = prog.plans, prog.pairs, prog.inlined, prog.merged
     functions = runtime.load_functions(prog.source, prog.names) if prog.names else {}
     runners = []
@@ -1535,6 +1941,7 @@ def _defer_runner(deferred: dict, k: int):
         deferred[k] = (inputs, outs)
 
     run.launches_nothing = True
+    run.writes_output = True  # by the run's launch
     return run
 
 

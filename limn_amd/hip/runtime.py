@@ -198,7 +198,12 @@ def has_hip() -> bool:
 # ---- hipRTC ----
 
 _programs: dict[str, dict[str, int]] = {}
-RTC_OPTIONS = (f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops")
+# Every floating-point operation of a generated kernel rounds on its own (no multiply-add
+# contraction), as the numpy device's do: whether the compiler fuses a product into a following
+# add otherwise depends on how many uses the product has, so the same nest gave different bits
+# alone and inside a row program, where a value computed by several members is shared.
+RTC_OPTIONS = (f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-ffp-contract=off",
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops")
 
 
 def rtc_version() -> str:

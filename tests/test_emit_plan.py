@@ -256,3 +256,48 @@ def test_a_large_sink_streams_its_stores():
     assert "__builtin_nontemporal_store" not in sources[realized(doubled.node)]
     assert "__builtin_nontemporal_store" not in sources[realized(small.node)]
     assert emit.streamed_outputs(nests, None, None) == set()
+
+
+# ---- row programs ----
+
+
+def test_softmax_layernorm_is_one_row_program():
+    """The five launching nests of a row softmax then LayerNorm (max, sum of exp, mean, sum of
+    squares, the final pass) run as one row program; a workgroup per row at 4096-wide rows, a
+    wave per row at 512."""
+    for n, group in ((4096, emit.THREADS), (512, 64)):
+        nests, kept = lowered([softmax_layernorm(n)])
+        prog = emit.plan_program(nests, kept, set())
+        assert len(prog.names) == 1 and "_rows_" in prog.names[0]
+        (run, _), = prog.merged.values()
+        assert [nests[c].kernel.ast.op for c in run][:4] == [Op.MAX, Op.SUM, Op.SUM, Op.SUM] and len(run) == 5
+        members = [emit.row_member(nests[c], prog.plans[c]) for c in run]
+        assert [m.kind for m in members] == ["reduce"] * 4 + ["cells"]
+        assert {m.group for m in members if m.kind == "reduce"} == {group}
+        assert "rv0_" in prog.source  # later members read the row max from a register
+        assert emit.plan_program(nests, kept, set(), rows=False).names != prog.names
+
+
+def test_a_bfloat16_layernorm_is_one_row_program():
+    from limn_amd.seam import nn
+    x = Tensor(rng.standard_normal((64, 512)).astype(np.float32), dtype=bfloat16)
+    nests, kept = lowered([nn.LayerNorm(512)(x)])
+    prog = emit.plan_program(nests, kept, set())
+    assert len(prog.names) == 1 and "_rows_" in prog.names[0]
+    assert "f2b(rv0_)" in prog.source  # the mean is read back rounded as its bf16 store rounds it
+
+
+def test_a_read_of_another_row_ends_the_row_program():
+    """A nest reading the row statistics along its columns (a transposed broadcast) cannot be a
+    member: the program ends before it and it launches on its own."""
+    n = 512
+    x = Tensor(rng.standard_normal((n, n)).astype(np.float32))
+    s = x.max(axis=-1, keepdim=True)
+    y = (x - s).exp().sum(axis=-1, keepdim=True)
+    z = x * y.reshape(1, n)
+    nests, kept = lowered([z])
+    prog = emit.plan_program(nests, kept, set())
+    runs = [run for run, _ in prog.merged.values()]
+    target = realized(z.node)
+    assert all(nests[c].kernel.target is not target for run in runs for c in run)
+    assert any(len(run) == 2 for run in runs)  # max and sum still share a row program

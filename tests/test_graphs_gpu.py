@@ -182,14 +182,24 @@ def launch_free_calls(hipdev, sinks) -> int:
 
 
 def test_softmax_layernorm_with_inlined_row_statistics(hipdev):
-    """The six per-row and scalar kernels of softmax -> LayerNorm run inside their readers; the
-    result still matches the oracle."""
-    x = Tensor(randf(300, 257))
-    y = x.softmax(-1)
-    c = y - y.mean(axis=-1, keepdim=True)
-    out = c / ((c * c).mean(axis=-1, keepdim=True) + 1e-5).sqrt()
-    assert launch_free_calls(hipdev, [out.node]) == 6
-    check(hipdev, out, rtol=1e-4, atol=1e-5)
+    """Without row programs the six per-row and scalar kernels of softmax -> LayerNorm run inside
+    their readers (four launches stay); with them the ten kernels run inside the last one's
+    launch. Both match the oracle."""
+    from limn_amd.hip.device import HipDevice
+
+    data = randf(300, 257)
+
+    def chain() -> Tensor:
+        y = Tensor(data).softmax(-1)
+        c = y - y.mean(axis=-1, keepdim=True)
+        return c / ((c * c).mean(axis=-1, keepdim=True) + 1e-5).sqrt()
+
+    plain = HipDevice()
+    plain.row_programs = False
+    assert launch_free_calls(plain, [chain().node]) == 6
+    check(plain, chain(), rtol=1e-4, atol=1e-5)
+    assert launch_free_calls(hipdev, [chain().node]) == 10
+    check(hipdev, chain(), rtol=1e-4, atol=1e-5)
 
 
 def test_inlined_producer_read_through_a_pad_and_a_gather_index(hipdev):
@@ -698,3 +708,54 @@ def test_column_max_keeps_nan(hipdev):
     x[3, 17, 5] = np.nan
     x[9, 100, 69] = np.nan
     check(hipdev, Tensor(x).max(axis=(0, 1)))
+
+
+# row programs: a chain of row reductions and their readers in one launch (emit.row_chains)
+
+
+def _softmax_layernorm(x: Tensor) -> Tensor:
+    y = x.softmax(-1)
+    c = y - y.mean(axis=-1, keepdim=True)
+    return c / ((c * c).mean(axis=-1, keepdim=True) + 1e-5).sqrt()
+
+
+def _layernorm(dtype, shape):
+    from limn_amd.seam import nn
+
+    def build(x):
+        t = Tensor(x, dtype=dtype)
+        return nn.LayerNorm(shape[-1])(t)
+
+    return build
+
+
+ROW_CASES = {
+    # a workgroup per row (5000-wide rows), 70 rows
+    "softmax_layernorm_wide": ((70, 5000), lambda x: _softmax_layernorm(Tensor(x))),
+    # odd width: one value per vector chunk, a wave per row
+    "softmax_layernorm_odd": ((33, 777), lambda x: _softmax_layernorm(Tensor(x))),
+    "layernorm_bf16": ((100, 512), _layernorm(bfloat16, (100, 512))),
+    "layernorm_f16_3d": ((4, 50, 256), _layernorm(float16, (4, 50, 256))),
+}
+
+
+@pytest.mark.parametrize("case", sorted(ROW_CASES))
+def test_row_programs_give_the_bits_of_separate_launches(hipdev, case):
+    """The fused row program stores exactly what the same nests launched one by one store
+    (same strided loops, vector widths and fold orders), and agrees with the numpy oracle."""
+    from limn_amd.dtypes import from_storage
+    from limn_amd.hip.device import HipDevice
+
+    shape, build = ROW_CASES[case]
+    x = randf(*shape)
+    plain = HipDevice()
+    plain.row_programs = False
+    outs = []
+    for dev in (hipdev, plain):
+        t = build(x)
+        outs.append(from_storage(dev.copyout(dev.execute([t.node])[0]), t.dtype, t.shape))
+    got, want = (np.ascontiguousarray(o).reshape(-1) for o in outs)
+    assert got.dtype == want.dtype and got.shape == want.shape
+    assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), case
+    half = case.startswith("layernorm")  # half-width x: every intermediate rounds to it
+    check(hipdev, build(x), rtol=2e-2 if half else 1e-4, atol=2e-2 if half else 1e-4)
