@@ -642,17 +642,27 @@ def bench_c5(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
         fn = capture(step)
         rng = np.random.default_rng(5)
         batches = [synthetic_batch(cfg, rng) for _ in range(4)]
-        for i in range(max(warmup, 3)):  # two observed calls, then replays
+        # two observed calls, then replays; a replay captures a graph per binding (a batch's
+        # buffers with one of the two output arenas that alternate while the previous step's
+        # loss is alive), every pair the rotation meets before the timed steps
+        done = max(warmup, 3 + 2 * len(batches))
+        for i in range(done):
             loss = fn(*batches[i % 4])
         first_loss = float(loss.item())
         dev.finish()
         issued = dev.issue_seconds
+
+        def captures() -> int:
+            return sum(e[1].captures for e in dev.replays.values() if e[1] is not None)
+
+        captured = captures()
         t0 = time.perf_counter()
-        for i in range(steps):
+        for i in range(done, done + steps):  # the batches in the same rotation as the warmup's
             loss = fn(*batches[i % 4])
         dev.finish()
         elapsed = time.perf_counter() - t0
         issue_ms = (dev.issue_seconds - issued) / steps * 1e3
+        captured = captures() - captured
         last_loss = float(loss.item())
     finally:
         limn_device.active_device = saved
@@ -693,6 +703,7 @@ def bench_c5(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
         "mfu": round(per_step * steps / elapsed / MFMA_BF16_PEAK, 4),
         "loss": {"after_warmup": round(first_loss, 4), "last": round(last_loss, 4)},
         "host_issue_ms_per_step": round(issue_ms, 3),
+        "graph_captures_timed": captured,
         "roofline": {"kernel": "whole step", "bound": "mfma", "achieved": round(per_step * steps / elapsed / 1e12, 2),
                      "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s", "frac": round(per_step * steps / elapsed / MFMA_BF16_PEAK, 4),
                      "traffic": None},

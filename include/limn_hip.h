@@ -168,6 +168,20 @@ typedef struct {
 int limn_hip_replay(const limn_hip_replay_step* steps, int64_t nsteps, const limn_hip_replay_arg* args, int64_t nargs,
                     const int64_t* slots, int64_t nslots, void* stream);
 
+/*
+ * The same list issued as a HIP graph on the null stream: the first call captures the steps,
+ * bound to `slots`, into a graph (recorded on a stream made for the capture, not run) and
+ * instantiates it; a later call with the same list and the same slot values launches the
+ * instantiated graph (one call for every launch of the list), and one with other slots captures
+ * again. `*handle` is NULL before the first call; limn_hip_replay_graph_free releases it, once no
+ * launch of it is pending. No counterpart in the reference (limn/capture.py:152-179 replays
+ * through every runner); for callers that replay one plan many times with the same buffers, such
+ * as a training loop.
+ */
+int limn_hip_replay_graph(const limn_hip_replay_step* steps, int64_t nsteps, const limn_hip_replay_arg* args,
+                          int64_t nargs, const int64_t* slots, int64_t nslots, void** handle);
+int limn_hip_replay_graph_free(void* handle);
+
 #ifdef __cplusplus
 }
 #endif

@@ -8,6 +8,8 @@
 
 #include <stdio.h>
 
+#include <vector>
+
 #include "matmul.h"
 #include "sdpa.h"
 
@@ -16,6 +18,27 @@ using namespace limn;
 namespace {
 
 constexpr int MAX_ARGS = 256;  // a merged launch of up to 16 nests takes at most a few dozen pointers
+
+// A zero fill as a kernel rather than hipMemsetAsync, so the list can be captured into a graph
+// (memset nodes of captured graphs have given wrong results on replays after the first): 16-byte
+// stores over the aligned body, single bytes at the ends.
+__global__ __launch_bounds__(256) void zero_bytes(unsigned char* __restrict__ p, int64_t n) {
+  const int64_t head = ((16 - ((uintptr_t)p & 15)) & 15) < n ? (16 - ((uintptr_t)p & 15)) & 15 : n;
+  const int64_t chunks = (n - head) / 16, tail = n - head - chunks * 16;
+  uint4* body = (uint4*)(p + head);
+  for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < chunks; i += (int64_t)gridDim.x * 256)
+    body[i] = make_uint4(0, 0, 0, 0);
+  if (blockIdx.x == 0 && threadIdx.x < head) p[threadIdx.x] = 0;
+  if (blockIdx.x == 0 && threadIdx.x < tail) p[head + chunks * 16 + threadIdx.x] = 0;
+}
+
+int zero_fill(void* p, int64_t n, hipStream_t stream) {
+  if (n <= 0) return LIMN_HIP_OK;
+  const int64_t blocks = (n / 16 + 255) / 256;
+  const unsigned grid = (unsigned)(blocks < 1 ? 1 : blocks > 4096 ? 4096 : blocks);
+  hipLaunchKernelGGL(zero_bytes, dim3(grid), dim3(256), 0, stream, (unsigned char*)p, n);
+  return check_hip(hipGetLastError(), "launching a replayed zero fill");
+}
 
 int64_t bound(const limn_hip_replay_arg& a, const int64_t* slots) { return a.slot < 0 ? a.value : slots[a.slot] + a.value; }
 
@@ -44,8 +67,7 @@ int run_step(const limn_hip_replay_step& s, int64_t i, const limn_hip_replay_arg
     case LIMN_HIP_STEP_ZERO: {
       int rc = expect(s, i, 2, "zero");
       if (rc != LIMN_HIP_OK) return rc;
-      return check_hip(hipMemsetAsync((void*)ptr(a[0], slots), 0, (size_t)bound(a[1], slots), (hipStream_t)stream),
-                       "zeroing a replayed output");
+      return zero_fill((void*)ptr(a[0], slots), bound(a[1], slots), (hipStream_t)stream);
     }
     case LIMN_HIP_STEP_MATMUL: {
       int rc = expect(s, i, 20, "matmul");
@@ -90,11 +112,10 @@ int run_step(const limn_hip_replay_step& s, int64_t i, const limn_hip_replay_arg
   }
 }
 
-}  // namespace
-
-extern "C" int limn_hip_replay(const limn_hip_replay_step* steps, int64_t nsteps, const limn_hip_replay_arg* args,
-                               int64_t nargs, const int64_t* slots, int64_t nslots, void* stream) {
-  if (nsteps < 0 || nargs < 0 || nslots < 0 || (nsteps > 0 && (steps == nullptr || args == nullptr)))
+int check_list(const limn_hip_replay_step* steps, int64_t nsteps, const limn_hip_replay_arg* args, int64_t nargs,
+               const int64_t* slots, int64_t nslots) {
+  if (nsteps < 0 || nargs < 0 || nslots < 0 || (nsteps > 0 && (steps == nullptr || args == nullptr)) ||
+      (nslots > 0 && slots == nullptr))
     return fail(LIMN_HIP_EINVAL, "replay: bad step or argument list");
   for (int64_t i = 0; i < nsteps; i++) {
     const limn_hip_replay_step& s = steps[i];
@@ -105,8 +126,98 @@ extern "C" int limn_hip_replay(const limn_hip_replay_step* steps, int64_t nsteps
       const int32_t slot = args[s.first + k].slot;
       if (slot >= nslots) return fail(LIMN_HIP_EINVAL, "replay step %lld: slot %d of %lld", (long long)i, slot, (long long)nslots);
     }
-    const int rc = run_step(s, i, args + s.first, slots, stream);
+  }
+  return LIMN_HIP_OK;
+}
+
+int run_list(const limn_hip_replay_step* steps, int64_t nsteps, const limn_hip_replay_arg* args, const int64_t* slots,
+             void* stream) {
+  for (int64_t i = 0; i < nsteps; i++) {
+    const int rc = run_step(steps[i], i, args + steps[i].first, slots, stream);
     if (rc != LIMN_HIP_OK) return rc;
   }
+  return LIMN_HIP_OK;
+}
+
+// A list captured as a graph and the binding it was captured with.
+struct ReplayGraph {
+  hipGraphExec_t exec = nullptr;
+  const limn_hip_replay_step* steps = nullptr;
+  const limn_hip_replay_arg* args = nullptr;
+  int64_t nsteps = 0, nargs = 0;
+  std::vector<int64_t> slots;
+
+  void drop_exec() {
+    if (exec != nullptr) hipGraphExecDestroy(exec);
+    exec = nullptr;
+  }
+
+  ~ReplayGraph() { drop_exec(); }
+
+  bool matches(const limn_hip_replay_step* s, int64_t ns, const limn_hip_replay_arg* a, int64_t na, const int64_t* sl,
+               int64_t nsl) const {
+    if (exec == nullptr || s != steps || ns != nsteps || a != args || na != nargs || (int64_t)slots.size() != nsl) return false;
+    for (int64_t i = 0; i < nsl; i++)
+      if (slots[(size_t)i] != sl[i]) return false;
+    return true;
+  }
+
+  // The steps recorded (not run) on a stream made for the capture: non-blocking, so the capture
+  // never meets the null stream's implicit synchronisation.
+  int capture(const limn_hip_replay_step* s, int64_t ns, const limn_hip_replay_arg* a, int64_t na, const int64_t* sl,
+              int64_t nsl) {
+    drop_exec();
+    hipStream_t stream = nullptr;
+    int rc = check_hip(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "creating a capture stream");
+    if (rc != LIMN_HIP_OK) return rc;
+    rc = check_hip(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "starting a replay capture");
+    if (rc == LIMN_HIP_OK) {
+      const int listed = run_list(s, ns, a, sl, stream);
+      hipGraph_t graph = nullptr;
+      rc = check_hip(hipStreamEndCapture(stream, &graph), "ending a replay capture");
+      if (listed != LIMN_HIP_OK) rc = listed;
+      if (rc == LIMN_HIP_OK) rc = check_hip(hipGraphInstantiateWithFlags(&exec, graph, 0), "instantiating a replay graph");
+      if (graph != nullptr) hipGraphDestroy(graph);
+    }
+    hipStreamDestroy(stream);
+    if (rc != LIMN_HIP_OK) {
+      exec = nullptr;
+      return rc;
+    }
+    steps = s;
+    nsteps = ns;
+    args = a;
+    nargs = na;
+    slots.assign(sl, sl + nsl);
+    return LIMN_HIP_OK;
+  }
+};
+
+}  // namespace
+
+extern "C" int limn_hip_replay(const limn_hip_replay_step* steps, int64_t nsteps, const limn_hip_replay_arg* args,
+                               int64_t nargs, const int64_t* slots, int64_t nslots, void* stream) {
+  const int rc = check_list(steps, nsteps, args, nargs, slots, nslots);
+  if (rc != LIMN_HIP_OK) return rc;
+  return run_list(steps, nsteps, args, slots, stream);
+}
+
+extern "C" int limn_hip_replay_graph(const limn_hip_replay_step* steps, int64_t nsteps, const limn_hip_replay_arg* args,
+                                     int64_t nargs, const int64_t* slots, int64_t nslots, void** handle) {
+  if (handle == nullptr) return fail(LIMN_HIP_EINVAL, "replay_graph: no handle");
+  int rc = check_list(steps, nsteps, args, nargs, slots, nslots);
+  if (rc != LIMN_HIP_OK) return rc;
+  ReplayGraph* g = (ReplayGraph*)*handle;
+  if (g == nullptr) *handle = g = new ReplayGraph();
+  if (!g->matches(steps, nsteps, args, nargs, slots, nslots)) {
+    rc = g->capture(steps, nsteps, args, nargs, slots, nslots);
+    if (rc != LIMN_HIP_OK) return rc;
+  }
+  // on the null stream, ordered as the steps themselves would be there
+  return check_hip(hipGraphLaunch(g->exec, nullptr), "launching a replay graph");
+}
+
+extern "C" int limn_hip_replay_graph_free(void* handle) {
+  delete (ReplayGraph*)handle;
   return LIMN_HIP_OK;
 }

@@ -72,6 +72,33 @@ class HipBuffer:
             pass
 
 
+class Arena:
+    """One allocation holding every output of a replay, kept by its launch list for later
+    replays; `live` counts the buffers handed out inside it that are still referenced."""
+
+    __slots__ = ("buf", "live")
+
+    def __init__(self, buf: HipBuffer):
+        self.buf = buf
+        self.live = 0
+
+
+class ArenaBuffer:
+    """Bytes inside a replay's arena. The arena is free for another replay once every buffer
+    inside it has dropped (later launches are ordered after the earlier ones on the stream)."""
+
+    __slots__ = ("ptr", "nbytes", "arena")
+
+    def __init__(self, ptr: int, nbytes: int, arena: Arena):
+        self.ptr = ptr
+        self.nbytes = nbytes
+        self.arena = arena
+        arena.live += 1
+
+    def __del__(self) -> None:
+        self.arena.live -= 1
+
+
 class HipDevice(CompiledDevice):
     """Construct through set_device("hip"), which checks the runtime and the GPU first."""
 
@@ -105,6 +132,7 @@ class HipDevice(CompiledDevice):
         # pre-bound launch lists: id(plan) -> [plan, Program or None, refused]; `tape` collects
         # the launches of the run that records one (every launch site appends while it is set)
         self.replays: dict[int, list] = {}
+        self.replay_graphs = True  # replay through a captured graph (False: launch by launch)
         self.tape: list[replay.Launch] | None = None
         self.issue_seconds = 0.0  # host time replayed runs spent before their barrier, summed
 
@@ -123,8 +151,11 @@ class HipDevice(CompiledDevice):
         return HipBuffer(ptr.value, nb, self.pool)
 
     def trim(self) -> None:
-        """Give every pooled buffer back to the runtime."""
+        """Give every pooled buffer, and every launch list's idle arenas, back to the runtime."""
         self.finish()
+        for entry in self.replays.values():
+            if entry[1] is not None:
+                entry[1].arenas = [a for a in entry[1].arenas if a.live]
         for ptrs in self.pool.values():
             for ptr in ptrs:
                 self.api.hipFree(ctypes.c_void_p(ptr))
@@ -167,11 +198,14 @@ class HipDevice(CompiledDevice):
         """The executor's transaction (every call, then the commits, then one barrier), issued
         one of three ways: a plan's first run call by call; its second also records every launch
         into a launch list (replay.py); later runs allocate fresh outputs, bind them and the
-        sources to the list's slots and launch it in one native call. Results and commits are
-        the same either way; a recording whose buffers overlap is refused and the plan keeps
-        running call by call."""
+        sources to the list's slots and launch it in one native call, as a graph captured for
+        that binding unless `replay_graphs` is off. Results and commits are the same either way;
+        a recording whose buffers overlap is refused and the plan keeps running call by call."""
         entry = self.replays.get(id(plan))
         if entry is None or entry[0] is not plan:
+            if entry is not None and entry[1] is not None:  # a dead plan's id, reused
+                self.finish()
+                entry[1].release(self.lib)
             self.replays[id(plan)] = [plan, None, False]
             return super().run(plan, sources)
         if entry[1] is not None:
@@ -213,23 +247,46 @@ class HipDevice(CompiledDevice):
         if bound is None:
             entry[2] = True
         else:
-            entry[1] = replay.Program(bound[0], bound[1], tuple(o.nbytes for o in outs_all), tuple(out_positions),
-                                      tuple(assigns), plan.positions)
+            nbytes = tuple(o.nbytes for o in outs_all)
+            offsets, total = replay.arena_layout(nbytes)
+            entry[1] = replay.Program(bound[0], bound[1], nbytes, tuple(out_positions), tuple(assigns), plan.positions,
+                                      offsets, total)
         return [bufs[p] for p in plan.sinks]
 
     def _replay(self, plan, prog: "replay.Program", sources):
         start = time.perf_counter()
         bufs: list = [None] * plan.positions
         slots = np.zeros(prog.nslots, dtype=np.int64)
+        sinks = set(plan.sinks)
         for p, buf in sources.items():
-            bufs[p] = self.prepare(buf)
+            if isinstance(buf, np.ndarray) and p not in sinks:
+                # host bytes go to the list's own buffer for this position (the copy waits for
+                # the launches before it), so a loop feeding host batches binds the same buffers
+                staged = prog.staging.get(p)
+                if staged is None or staged.nbytes != buf.nbytes:
+                    staged = prog.staging[p] = self._alloc(buf.nbytes)
+                self.copyin(staged, buf)
+                bufs[p] = staged
+            else:
+                bufs[p] = self.prepare(buf)
             slots[p] = bufs[p].ptr
-        outs = [self._alloc(nb) for nb in prog.out_nbytes]  # zero fills are steps of the list
+        # the list's own arenas, one not in use: the same few bindings recur step after step
+        # whatever else the pool hands out between them (zero fills are steps of the list)
+        arena = next((a for a in prog.arenas if a.live == 0), None)
+        if arena is None:
+            arena = Arena(self._alloc(prog.arena_bytes))
+            if len(prog.arenas) < replay.ARENAS_PER_PLAN:
+                prog.arenas.append(arena)
+        outs = [ArenaBuffer(arena.buf.ptr + off, nb, arena) for off, nb in zip(prog.arena_offsets, prog.out_nbytes)]
+        del arena
         for i, out in enumerate(outs):
             slots[prog.positions + i] = out.ptr
         for i, p in prog.out_positions:
             bufs[p] = outs[i]
-        check_limn(prog.launch(self.lib, slots))
+        if self.replay_graphs:
+            check_limn(prog.launch_graph(self.lib, slots, self.finish))
+        else:
+            check_limn(prog.launch(self.lib, slots))
         for p, i in prog.assigns:
             self.commit(sources[p], outs[i])
             bufs[p] = outs[i]

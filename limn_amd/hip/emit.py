@@ -524,6 +524,42 @@ def run_loads(nest: LoopNest, body: list[Instr], bufs: Buffers, var: str, vec: i
     return pre, runs
 
 
+def prefetch_row(body: list[Instr], bufs: Buffers, var: str, vec: int, tag: str,
+                 indent: str) -> tuple[list[str], list[str], dict[str, str]]:
+    """The plain (unmasked) loads of a nest body for one run of `vec` values of `var`, as
+    registers filled ahead of the arithmetic: their declarations, the loads (in the scope where
+    the loop variables are decoded and `var`_b is set) and the `Buffers.cached` entries that make
+    the body read them."""
+    decls: list[str] = []
+    loads: list[str] = []
+    cached: dict[str, str] = {}
+    for instr in body:
+        if instr.opcode is not Opcode.LOAD:
+            continue
+        buf, index, valid = instr.arg
+        if buf in bufs.inline or buf in bufs.rowvals or valid.bounds:
+            continue
+        dt, d = bufs.dtypes[buf], instr.dest
+        st, reg = STORE_T[dt], f"{tag}{instr.dest}"
+        steps = dict(index.terms).get(var)
+        if steps is None:
+            decls.append(f"{st} {reg};")
+            loads.append(f"{indent}{reg} = {buf}[{render_index(index, bufs.wide_index)}];")
+            cached[d] = load_expr(dt, reg)
+            continue
+        decls.append(f"{st} {reg}[{vec}];")
+        if steps == 1:
+            loads.append(f"{indent}{{ const {st}* p_ = {buf} + (i64)({run_start(index, var, vec)});")
+            loads.append(f"{indent}#pragma unroll")
+            loads.append(f"{indent}  for (int j_ = 0; j_ < {vec}; j_++) {reg}[j_] = p_[j_]; }}")
+        else:
+            loads.append(f"{indent}#pragma unroll")
+            loads.append(f"{indent}for (int j_ = 0; j_ < {vec}; j_++) {{ const int {var} = {var}_b * {vec} + j_; "
+                         f"{reg}[j_] = {buf}[{render_index(index, True)}]; }}")
+        cached[d] = load_expr(dt, f"{reg}[j_]")
+    return decls, loads, cached
+
+
 def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers, stream: bool = False) -> Planned:
     """One thread per run of `vec` output cells, grid-strided. With `stream`, the output goes
     out through non-temporal stores (see STREAM_BYTES)."""
@@ -1011,8 +1047,16 @@ def fold_parts(name: str, shape: NestShape, acc_t: str, out_dtype: DType, out_re
     wave_fold = "wave_fold_add" if fold is Op.ADD else "wave_fold_max"
     lines.append("  const int lane = threadIdx.x & 63;")
     lines.append(f"  for (i64 g = blockIdx.x * (i64){waves} + (threadIdx.x >> 6); g < {cells}LL; g += (i64)gridDim.x * {waves}) {{")
+    # each lane's parts loaded together (the last run clamped into range), then folded in order
     lines.append(f"    {acc_t} acc = {ident};")
-    lines.append(f"    for (int p_ = lane; p_ < {parts}; p_ += 64) " + _fold(fold, "acc", f"scratch[{at}]"))
+    steps = -(-parts // 64)
+    for q in range(steps):
+        clamp = f"lane + {64 * q} < {parts} ? lane + {64 * q} : {parts - 1}" if 64 * (q + 1) > parts else f"lane + {64 * q}"
+        lines.append(f"    {acc_t} f{q}_;")
+        lines.append(f"    {{ const int p_ = {clamp}; f{q}_ = scratch[{at}]; }}")
+    for q in range(steps):
+        step = _fold(fold, "acc", f"f{q}_")
+        lines.append(f"    if (lane + {64 * q} < {parts}) {step}" if 64 * (q + 1) > parts else f"    {step}")
     lines.append(f"    acc = {wave_fold}(acc);")
     lines.append("    if (lane == 0) {")
     lines += decode(shape.outer, "g", "      ", wide)
@@ -1024,6 +1068,7 @@ def fold_parts(name: str, shape: NestShape, acc_t: str, out_dtype: DType, out_re
 COLUMN_TILE = 64  # cells per workgroup of a column reduce: one wave's lanes, one coalesced row piece
 COLUMN_BLOCKS = 2048  # workgroups a column reduce aims for (8 per CU): tiles x row parts
 COLUMN_ROWS = 16  # the fewest rows a wave of a column reduce folds
+COLUMN_UNROLL = 8  # rows a wave of a column reduce loads at once
 
 
 def plan_columns(nest: LoopNest, shape: NestShape, bufs: Buffers, cells: int, R: int) -> Planned:
@@ -1068,15 +1113,52 @@ def plan_columns(nest: LoopNest, shape: NestShape, bufs: Buffers, cells: int, R:
     lines.append(f"  if (gb < {cells // vec}LL) {{")
     lines += decode(base_vars, "gb", "    ", wide)
     lines.append(f"    const i64 stop_ = (p_ + 1) * {per_part}LL < {R}LL ? (p_ + 1) * {per_part}LL : {R}LL;")
-    lines.append(f"    for (i64 r_ = p_ * {per_part}LL + wave; r_ < stop_; r_ += {waves}) {{")
-    lines += decode(shape.inner, "r_", "      ", True)
-    lines += pre
-    lines.append("#pragma unroll")
-    lines.append(f"      for (int j_ = 0; j_ < {vec}; j_++) {{")
-    lines.append(f"        const int {along} = {along}_b * {vec} + j_;")
-    lines += body
-    lines.append("        " + _fold(fold, "acc[j_]", f"({acc_t}){shape.item}"))
-    lines += ["      }", "    }", "  }"]
+    lines.append(f"    i64 r_ = p_ * {per_part}LL + wave;")
+
+    def row(var: str, indent: str) -> list[str]:
+        """One row's loads and its fold into acc, in scope of its own."""
+        out = [indent + "{"]
+        out += decode(shape.inner, var, indent + "  ", True)
+        out += [indent + ln[6:] for ln in pre]
+        out.append("#pragma unroll")
+        out.append(f"{indent}  for (int j_ = 0; j_ < {vec}; j_++) {{")
+        out.append(f"{indent}    const int {along} = {along}_b * {vec} + j_;")
+        out += [indent + ln[6:] for ln in body]
+        out.append(f"{indent}    " + _fold(fold, "acc[j_]", f"({acc_t}){shape.item}"))
+        out += [f"{indent}  }}", indent + "}"]
+        return out
+
+    # COLUMN_UNROLL of the wave's rows per step: every row's loads first, into registers, then
+    # each row folded in order from them, so the rows' loads are in flight together (a row at a
+    # time, a wave waits out the memory latency once per row); then the rest one at a time
+    unroll = max(1, min(COLUMN_UNROLL, per_part // waves))
+    if unroll > 1:
+        lines.append(f"    for (; r_ + {(unroll - 1) * waves} < stop_; r_ += {unroll * waves}) {{")
+        fetched = []
+        for u in range(unroll):
+            lines.append(f"      const i64 r{u}_ = r_ + {u * waves};")
+            decls, loads, cached = prefetch_row(shape.body, bufs, along, vec, f"ra{u}_", "        ")
+            lines += ["      " + d for d in decls]
+            lines.append("      {")
+            lines += decode(shape.inner, f"r{u}_", "        ", True)
+            lines += loads
+            lines.append("      }")
+            fetched.append(cached)
+        for u in range(unroll):
+            bufs.cached = fetched[u]
+            lines.append("      {")
+            lines += decode(shape.inner, f"r{u}_", "        ", True)
+            lines.append("#pragma unroll")
+            lines.append(f"        for (int j_ = 0; j_ < {vec}; j_++) {{")
+            lines.append(f"          const int {along} = {along}_b * {vec} + j_;")
+            lines += ["          " + value_line(i, bufs) for i in shape.body]
+            lines.append("          " + _fold(fold, "acc[j_]", f"({acc_t}){shape.item}"))
+            lines += ["        }", "      }"]
+        bufs.cached = {}
+        lines.append("    }")
+    lines.append(f"    for (; r_ < stop_; r_ += {waves}) {{")
+    lines += row("r_", "      ")
+    lines += ["    }", "  }"]
     # the waves' totals for each lane's cells, folded in wave order
     lines.append(f"  __shared__ {acc_t} lds_[{waves}][{64 * vec}];")
     lines.append("#pragma unroll")
@@ -1597,11 +1679,13 @@ def row_chains(nests: list[LoopNest], plans: list[Planned], custom_inputs: set |
     return chains
 
 
-# A row program keeps the row of an input that two or more members read at (row, cell) in
-# registers, up to this many values a thread: the row comes from HBM once and every later pass
-# over it reads the registers. Re-read from memory, the passes of an 8192-float row softmax then
-# LayerNorm (32 KB a row, thousands of rows in flight) missed the L2 and ran at 2.5 TB/s of
-# algorithmic bytes; the row is 32 values a thread of a 256-thread workgroup.
+# A row program keeps the row of each input its members read at (row, cell) in registers, up
+# to this many values a thread, loaded when the row starts: the row comes from HBM once, every
+# later pass over it reads the registers, and the loads of all the inputs are in flight together
+# (an input first read by the last member would otherwise wait for the reductions before it).
+# Re-read from memory, the passes of an 8192-float row softmax then LayerNorm (32 KB a row,
+# thousands of rows in flight) missed the L2 and ran at 2.5 TB/s of algorithmic bytes; the row
+# is 32 values a thread of a 256-thread workgroup.
 ROW_CACHE_VALUES = 32
 
 
@@ -1622,8 +1706,8 @@ def _row_read(instr: Instr, inputs: list, member: RowMember):
 def row_source(name: str, nests: list[LoopNest], plans: list[Planned], run: list[int], inlined: "InlineSet",
                streamed: set[int]) -> tuple[str, int]:
     """One kernel for a row program (see row_chains): each member's parameters bound as its own
-    kernel's, its code for one row, in order, inside one loop over the rows. Inputs that several
-    members read along the row are loaded into registers once per row (ROW_CACHE_VALUES); the
+    kernel's, its code for one row, in order, inside one loop over the rows. The inputs the members
+    read along the row are loaded into registers when the row starts (ROW_CACHE_VALUES); the
     members' loops then run unrolled over the same cells in the same order, so every fold adds in
     the order of the member's own kernel."""
     members = [(c, row_member(nests[c], plans[c])) for c in run]
@@ -1657,7 +1741,7 @@ def row_source(name: str, nests: list[LoopNest], plans: list[Planned], run: list
         vec = setup[slots[0]][1]
         same = [s_ for s_ in slots if setup[s_][1] == vec]
         passes = -(-(cols // vec) // threads)
-        if len(same) < 2 or passes * vec > room:
+        if passes * vec > room:
             continue
         room -= passes * vec
         cache[node] = (f"rc{len(cache)}_", vec, passes, same)

@@ -7,8 +7,12 @@ milliseconds per step. The hip device instead records a hot plan's launches once
 ordinary run with every buffer of the run kept alive: each launch becomes a step of
 `limn_hip_replay` (include/limn_hip.h) and each argument either a constant (a size, a kernel's
 own scratch pointer) or an offset into a *slot*: a buffer position of the plan (its sources) or
-one of the outputs the run allocated, in call order. A replay allocates fresh outputs, binds every
-slot to this run's buffer and issues the whole list in one call.
+one of the outputs the run allocated, in call order. A replay takes its outputs from one arena
+(fixed offsets in one allocation the list keeps, reused once nothing inside it is referenced, so
+the same few bindings recur run after run), binds every
+slot to this run's buffer and issues the whole list in one call: as a HIP graph captured for that
+binding (one capture serves every later run with the same buffers, and the launches cost the host
+one call), or launch by launch.
 
 A recording is refused (the plan keeps running call by call) when two slots share bytes, since a
 pointer into them could not be told apart.
@@ -17,7 +21,8 @@ pointer into them could not be told apart.
 from __future__ import annotations
 
 import bisect
-from dataclasses import dataclass
+import ctypes
+from dataclasses import dataclass, field
 
 import numpy as np
 
@@ -59,6 +64,14 @@ class Program:
     out_positions: tuple[tuple[int, int], ...]  # (output index, plan position) of outputs the plan reads
     assigns: tuple[tuple[int, int], ...]  # (target position, output index) committed after the list
     positions: int  # slots [0, positions) are the plan's buffer positions, then the outputs
+    arena_offsets: tuple[int, ...] = ()  # each output's byte offset in the replay's one allocation
+    arena_bytes: int = 0
+    # captured graphs by binding (slot values), the most recently used last; a training loop that
+    # keeps the previous step's result alive while it runs the next alternates two bindings
+    graphs: dict[bytes, ctypes.c_void_p] = field(default_factory=dict)
+    captures: int = 0  # graphs captured
+    arenas: list = field(default_factory=list)  # the device's Arena objects for this list's outputs
+    staging: dict = field(default_factory=dict)  # plan position -> the buffer host bytes are copied to
 
     @property
     def nslots(self) -> int:
@@ -67,6 +80,43 @@ class Program:
     def launch(self, lib, slots: np.ndarray, stream=None) -> int:
         return lib.limn_hip_replay(self.steps.ctypes.data, len(self.steps), self.args.ctypes.data, len(self.args),
                                    slots.ctypes.data, len(slots), stream)
+
+    def launch_graph(self, lib, slots: np.ndarray, finish) -> int:
+        """The list as one graph launch on the null stream: the graph captured for this binding,
+        or a new capture (the least recently used of GRAPHS_PER_PLAN dropped first, after
+        `finish()` has waited for its launches)."""
+        key = slots.tobytes()
+        handle = self.graphs.pop(key, None)
+        if handle is None:
+            if len(self.graphs) >= GRAPHS_PER_PLAN:
+                finish()
+                lib.limn_hip_replay_graph_free(self.graphs.pop(next(iter(self.graphs))))
+            handle = ctypes.c_void_p()
+            self.captures += 1
+        self.graphs[key] = handle
+        return lib.limn_hip_replay_graph(self.steps.ctypes.data, len(self.steps), self.args.ctypes.data, len(self.args),
+                                         slots.ctypes.data, len(slots), ctypes.byref(handle))
+
+    def release(self, lib) -> None:
+        """Free the captured graphs (after the device has finished every launch of them)."""
+        for handle in self.graphs.values():
+            if handle.value:
+                lib.limn_hip_replay_graph_free(handle)
+        self.graphs.clear()
+
+
+GRAPHS_PER_PLAN = 8
+ARENAS_PER_PLAN = 3  # a list keeps this many output arenas; past that a replay takes a passing one
+ARENA_ALIGN = 256  # bytes between the starts of a replay's outputs in its arena
+
+
+def arena_layout(out_nbytes) -> tuple[tuple[int, ...], int]:
+    """Byte offsets of a replay's outputs in one allocation, and its size."""
+    offsets, at = [], 0
+    for nb in out_nbytes:
+        offsets.append(at)
+        at += -(-max(nb, 1) // ARENA_ALIGN) * ARENA_ALIGN
+    return tuple(offsets), max(at, 1)
 
 
 def bind(tape: list[Launch], slots: list[tuple[int, int, int]]) -> tuple[np.ndarray, np.ndarray] | None:

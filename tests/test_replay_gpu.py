@@ -67,3 +67,33 @@ def test_replayed_runs_equal_call_by_call_runs(hipdev, case):
             assert g.dtype == w.dtype and g.shape == w.shape
             np.testing.assert_array_equal(g.view(np.uint8), w.view(np.uint8))
     assert sum(e[1] is not None for e in hipdev.replays.values()) > before  # a list was recorded and replayed
+
+
+@pytest.mark.parametrize("case", sorted(CASES))
+def test_graph_replays_equal_call_by_call_runs(case):
+    """The launch list replayed as a captured HIP graph: six runs with new inputs, each checked bit
+    for bit against a device running call by call (eager work and its barriers between the
+    replays). Runs 3 and 4 keep their results alive, so the next runs get other buffers and the
+    graph is captured again for the new binding."""
+    from limn_amd.hip.device import HipDevice
+
+    graphs = HipDevice()
+    assert graphs.replay_graphs
+    plain = HipDevice()
+    plain.run = lambda plan, sources: CompiledDevice.run(plain, plan, sources)
+    held = []
+    for seed in range(6):
+        print(f"graph replay case {case}, run {seed}", flush=True)
+        limn_device.active_device = graphs
+        tensors = CASES[case](seed)
+        realize(*tensors)
+        got = [t.numpy() for t in tensors]
+        if seed in (3, 4):
+            held.append(tensors)
+        want = results(plain, CASES[case], seed)
+        for g, w in zip(got, want):
+            assert g.dtype == w.dtype and g.shape == w.shape
+            np.testing.assert_array_equal(g.view(np.uint8), w.view(np.uint8))
+    progs = [e[1] for e in graphs.replays.values() if e[1] is not None]
+    assert any(p.graphs for p in progs)  # graphs were captured and replayed
+    assert max(p.captures for p in progs) >= 2  # and captured again for the held runs' successors
