@@ -1404,22 +1404,26 @@ def inline_producers(nests: list[LoopNest], plans: list[Planned], kept: set | No
 MERGE_GRID = 1 << 16  # the largest elementwise launch merged with its neighbours
 MERGE_GROUP_GRID = 1 << 20  # the most workgroups of one merged launch
 MERGE_MEMBERS = 16  # the most nests in one merged launch
+MERGE_PARAMS = 160  # the most pointers one merged launch takes
 
 
 def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set | None, inlined: "InlineSet",
-               pairs: dict[int, int], taken: set[int] = frozenset()) -> list[list[int]]:
-    """Groups of small elementwise nests that can share one launch, made at the place of the
-    group's last member. A member joins when it reads no other member's output (directly or
-    through an inlined producer); a nest between members that is not one may stay between them
-    if it reads no member's output either (it launches at its own place, before the group), and
-    one that does ends the group. No member's output is read by a CUSTOM call, which may sit
-    between nests. Each member is at most MERGE_GRID workgroups, a group at most MERGE_MEMBERS
-    nests and MERGE_GROUP_GRID workgroups. An optimizer step gives such groups across parameters (each parameter's moments, then
-    the parameter from the new moments, with the next parameter's gradient reduce between):
-    launches of a few microseconds each for the small parameters. Nests in `taken` (members of
-    row programs) never join. `custom_inputs` None merges nothing."""
+               pairs: dict[int, int], taken: set[int] = frozenset()) -> tuple[list[list[int]], list[int]]:
+    """Groups of small elementwise nests that share one launch, and the nest whose runner
+    launches each. Several groups are open at once, in creation order: a nest joins the first
+    open group after every group holding a nest it reads (directly or through an inlined
+    producer), so a group only reads groups created before it; a group launches at the latest of
+    its last member and the launches of the groups it reads. A nest that is no member (it runs
+    at its own place) and reads a member closes that member's group and the groups that one
+    reads, which have all launched by then. No member's output is read by a CUSTOM call, which may
+    sit between nests. Each member is at most MERGE_GRID workgroups, a group at most
+    MERGE_MEMBERS nests, MERGE_PARAMS pointers and MERGE_GROUP_GRID workgroups. An optimizer step
+    gives groups across parameters: every parameter's moments in a first few groups, every
+    parameter's update from its new moments in the next few, where a run of consecutive nests
+    took a launch per parameter. Nests in `taken` (members of row programs) never join.
+    `custom_inputs` None merges nothing."""
     if custom_inputs is None:
-        return []
+        return [], []
     fused = set(pairs) | set(pairs.values())
 
     def reads(c: int) -> set:
@@ -1428,15 +1432,19 @@ def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set |
             nodes |= set(nests[j].kernel.inputs)
         return nodes
 
-    runs: list[list[int]] = []
-    run: list[int] = []
-    made: set = set()
+    groups: list[list[int]] = []
+    size: list[list[int]] = []  # [workgroups, pointers] per group
+    closed: list[bool] = []
+    deps: list[set[int]] = []
+    owner: dict = {}  # a member's output -> its group
 
-    def close() -> None:
-        if len(run) > 1:
-            runs.append(list(run))
-        run.clear()
-        made.clear()
+    def close(g: int) -> None:
+        stack = [g]
+        while stack:
+            h = stack.pop()
+            if not closed[h]:
+                closed[h] = True
+                stack.extend(deps[h])
 
     for c, (nest, plan) in enumerate(zip(nests, plans)):
         if c in inlined.producers:
@@ -1449,15 +1457,35 @@ def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set |
             and plan.launches[0].grid <= MERGE_GRID
             and nest.kernel.target not in custom_inputs
         )
-        depends = bool(reads(c) & made)
-        grid = plan.launches[0].grid if ok else 0
-        if depends or len(run) >= MERGE_MEMBERS or sum(plans[m].launches[0].grid for m in run) + grid > MERGE_GROUP_GRID:
-            close()
-        if ok:
-            run.append(c)
-            made.add(nest.kernel.target)
-    close()
-    return runs
+        hit = {owner[n] for n in reads(c) if n in owner}
+        if not ok:
+            for g in hit:
+                close(g)
+            continue
+        grid, params = plan.launches[0].grid, len(plan.notes["params"])
+        lo = max(hit) + 1 if hit else 0
+        target = next((g for g in range(lo, len(groups)) if not closed[g] and len(groups[g]) < MERGE_MEMBERS
+                       and size[g][0] + grid <= MERGE_GROUP_GRID and size[g][1] + params <= MERGE_PARAMS), None)
+        if target is None:
+            groups.append([])
+            size.append([0, 0])
+            closed.append(False)
+            deps.append(set())
+            target = len(groups) - 1
+        groups[target].append(c)
+        size[target][0] += grid
+        size[target][1] += params
+        deps[target] |= hit
+        owner[nest.kernel.target] = target
+    launch_at: list[int] = []
+    for g, members in enumerate(groups):
+        launch_at.append(max([members[-1]] + [launch_at[d] for d in deps[g]]))
+    # a lone member launching at its own place runs as an ordinary launch, unless other groups
+    # launch from its runner
+    hosts = [launch_at.count(at) for at in launch_at]
+    keep = [g for g, members in enumerate(groups)
+            if len(members) > 1 or launch_at[g] != members[-1] or hosts[g] > 1]
+    return [groups[g] for g in keep], [launch_at[g] for g in keep]
 
 
 def merged_source(name: str, nests: list[LoopNest], plans: list[Planned], run: list[int]) -> tuple[str, int]:
@@ -1913,16 +1941,26 @@ class Program:
     merged: dict[int, tuple[list[int], Launch]]
     source: str
     names: list[str]
+    # the nest whose runner launches each merged run (keyed as `merged`); a run missing here
+    # launches from its last member's
+    launch_at: dict[int, int] = field(default_factory=dict)
+
+    def launcher_of(self, key: int) -> int:
+        return self.launch_at.get(key, key)
+
+    def launches_from(self, k: int) -> list[int]:
+        """The merged runs (their keys, in launch order) that nest k's runner launches."""
+        return [key for key in self.merged if self.launcher_of(key) == k]
 
     def role(self, k: int) -> str:
         """What nest k's runner does: 'stash' (a contraction whose relu nest launches it),
-        'epilogue', 'inlined', 'deferred' (a merged run's earlier member), 'merged' (the run's
-        launch), 'contraction' or 'launch'."""
+        'epilogue', 'inlined', 'deferred' (a merged run's member whose runner launches nothing),
+        'merged' (it launches merged runs), 'contraction' or 'launch'."""
         if k in self.pairs:
             return "stash"
         if k in self.inlined.producers:
             return "inlined"
-        if k in self.merged:
+        if self.launches_from(k):
             return "merged"
         if any(k in run for run, _ in self.merged.values()):
             return "deferred"
@@ -1953,8 +1991,9 @@ def plan_program(nests: list[LoopNest], kept: set | None, custom_inputs: set | N
     for j in inlined.producers:
         plans[j] = Planned("", [], notes={"inlined": True})
     chains = row_chains(nests, plans, custom_inputs, inlined, pairs) if rows else []
-    runs = merge_runs(nests, plans, custom_inputs, inlined, pairs, {c for chain in chains for c in chain})
+    runs, run_launch = merge_runs(nests, plans, custom_inputs, inlined, pairs, {c for chain in chains for c in chain})
     merged: dict[int, tuple[list[int], Launch]] = {}
+    launch_at: dict[int, int] = {}
     merged_sources = []
     for chain in chains:
         name = f"{nests[chain[0]].name}_rows_{nests[chain[-1]].name}"
@@ -1962,17 +2001,18 @@ def plan_program(nests: list[LoopNest], kept: set | None, custom_inputs: set | N
         merged_sources.append(source)
         merged[chain[-1]] = (chain, Launch(name, grid, THREADS, "merged"))
     runs_all = runs + chains
-    for run in runs:
+    for run, at in zip(runs, run_launch):
         name = f"{nests[run[0]].name}_to_{nests[run[-1]].name}"
         source, grid = merged_source(name, nests, plans, run)
         merged_sources.append(source)
         merged[run[-1]] = (run, Launch(name, grid, THREADS, "merged"))
+        launch_at[run[-1]] = at
     in_run = {c for run in runs_all for c in run}
     names = [launch.name for k, p in enumerate(plans) if k not in in_run for launch in p.launches]
     names += [launch.name for _, launch in merged.values()]
     kept_sources = [p.source for k, p in enumerate(plans) if k not in in_run]
     source = PRELUDE + "\n".join(kept_sources + merged_sources) if names else ""
-    return Program(plans, pairs, inlined, merged, source, names)
+    return Program(plans, pairs, inlined, merged, source, names, launch_at)
 
 
 def nest_runners(dev, nests: list[LoopNest]):
@@ -1996,10 +2036,12 @@ def nest_runners(dev, nests: list[LoopNest]):
         elif role == "inlined":
             runners.append(_keep_runner(producer_inputs, k))
         elif role == "merged":
-            run, launch = merged[k]
-            count = sum(len(plans[c].notes["params"]) for c in run)
-            runners.append(_merged_runner(_launcher(dev, functions[launch.name], launch, count - 1), run, nests, inlined,
-                                          producer_inputs, deferred, k))
+            launches = []
+            for key in prog.launches_from(k):
+                run, launch = merged[key]
+                count = sum(len(plans[c].notes["params"]) for c in run)
+                launches.append((_launcher(dev, functions[launch.name], launch, count - 1), run))
+            runners.append(_merged_runner(launches, nests, inlined, producer_inputs, deferred, k))
         elif role == "deferred":
             runners.append(_defer_runner(deferred, k))
         elif role == "epilogue":
@@ -2029,21 +2071,23 @@ def _defer_runner(deferred: dict, k: int):
     return run
 
 
-def _merged_runner(launch, members: list[int], nests: list[LoopNest], inlined: "InlineSet", producer_inputs: dict,
+def _merged_runner(launches: list, nests: list[LoopNest], inlined: "InlineSet", producer_inputs: dict,
                    deferred: dict, k: int):
-    """A merged run's last member: one launch over every member's buffers, in parameter order
-    (inputs, an inlined producer's inputs, out)."""
-    extras = {c: inlined.extras(nests[c]) for c in members}
+    """The runner that launches merged runs, (launch, members) in order, nest k among their
+    members: one launch per run over every member's buffers, in parameter order (inputs, an
+    inlined producer's inputs, out)."""
+    extras = {c: inlined.extras(nests[c]) for _, members in launches for c in members}
 
     def run(inputs: list, outs: list) -> None:
         deferred[k] = (inputs, outs)
-        ptrs: list[int] = []
-        for c in members:
-            ins, outs_c = deferred.pop(c)
-            ptrs += [b.ptr for b in ins]
-            ptrs += [producer_inputs[j][m].ptr for j, m in extras[c]]
-            ptrs.append(outs_c[0].ptr)
-        launch(ptrs)
+        for launch, members in launches:
+            ptrs: list[int] = []
+            for c in members:
+                ins, outs_c = deferred.pop(c)
+                ptrs += [b.ptr for b in ins]
+                ptrs += [producer_inputs[j][m].ptr for j, m in extras[c]]
+                ptrs.append(outs_c[0].ptr)
+            launch(ptrs)
 
     return run
 

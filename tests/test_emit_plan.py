@@ -201,7 +201,7 @@ def runs_of(sinks: list[Tensor]):
     plans = [emit.plan_nest(n) for n in nests]
     pairs = emit.epilogue_pairs(nests, plans, kept)
     inl = emit.InlineSet(nests, emit.inline_producers(nests, plans, kept, pairs))
-    return nests, emit.merge_runs(nests, plans, custom, inl, pairs)
+    return nests, emit.merge_runs(nests, plans, custom, inl, pairs)[0]
 
 
 def test_independent_small_updates_share_a_launch():
@@ -221,11 +221,41 @@ def test_independent_small_updates_share_a_launch():
     )
 
 
+def test_an_optimizer_step_groups_across_parameters():
+    """Each parameter's moments read only old state and the gradient; its update reads the new
+    moments. The moments of every parameter share a group and the updates a later one, which
+    launches after the moments' group (as a run of consecutive nests, a launch per parameter)."""
+    n = 6
+    params = [Tensor(rng.standard_normal((64,)).astype(np.float32)) for _ in range(n)]
+    grads = [Tensor(rng.standard_normal((64,)).astype(np.float32)) for _ in range(n)]
+    moms = [Tensor(rng.standard_normal((64,)).astype(np.float32)) for _ in range(n)]
+    sinks = []
+    for p, g, m in zip(params, grads, moms):
+        m_new = m * 0.9 + g * 0.1
+        sinks += [m_new, p - m_new * 0.01]
+    nodes = [t.node for t in sinks]
+    order = topological(nodes)
+    nests = lower_all(nodes, order, schedule(nodes, order))
+    kept = {realized(s) for s in nodes}
+    prog = emit.plan_program(nests, kept, set())
+    runs = {key: run for key, (run, _) in prog.merged.items()}
+    assert len(runs) == 2
+    made = {nests[c].kernel.target: key for key, run in runs.items() for c in run}
+    first, second = runs
+    assert all(made.get(src) != second for c in runs[first] for src in nests[c].kernel.inputs)
+    assert any(made.get(src) == first for c in runs[second] for src in nests[c].kernel.inputs)
+    assert prog.launcher_of(first) < prog.launcher_of(second) or (
+        prog.launcher_of(first) == prog.launcher_of(second) and list(prog.launches_from(prog.launcher_of(first))) == [first, second])
+    # every nest of the plan is a member of one of the two groups, launched by two runners
+    assert sorted(c for run in runs.values() for c in run) == list(range(len(nests)))
+    assert sum(len(prog.launches_from(k)) for k in range(len(nests))) == 2
+
+
 def test_nothing_merges_without_a_record_of_custom_inputs():
     params = [Tensor(rng.standard_normal((64,)).astype(np.float32)) for _ in range(2)]
     nests, _ = lowered([p * 2.0 for p in params])
     plans = [emit.plan_nest(n) for n in nests]
-    assert emit.merge_runs(nests, plans, None, emit.InlineSet(nests, set()), {}) == []
+    assert emit.merge_runs(nests, plans, None, emit.InlineSet(nests, set()), {}) == ([], [])
 
 
 def test_merged_kernel_binds_each_members_buffers():
