@@ -434,6 +434,8 @@ def bench_c2(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     dom = int(np.argmax(per))
     achieved = kernels[dom]["bytes"] / (per[dom] * 1e-3)
     assert "ms" in kernels[dom]
+    kernel_name = (getattr(plan.calls[dom].fn, "kernels", None) or (f"k{dom}",))[-1]
+    kernels[dom]["kernel"] = kernel_name
 
     def build():
         x = Tensor(np.random.default_rng(2).standard_normal((N, N), dtype=np.float32))
@@ -452,13 +454,13 @@ def bench_c2(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
         "config": {"workload": f"C2 row softmax -> LayerNorm, x f32 (8192, 8192), {ncalls} scheduled kernels, {launched} launched", "bytes_per_step": total},
         "kernels": kernels,
         "roofline": {
-            "kernel": f"k{dom}",
+            "kernel": kernel_name,
             "bound": "hbm",
             "achieved": round(achieved / 1e9, 1),
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK, 4),
-            "traffic": traffic(f"c2:k{dom}"),
+            "traffic": traffic(f"c2:{kernel_name}"),
             "traffic_source": traffic_source(),
         },
         "cpu_baseline": None if cpu_s is None else {

@@ -2057,6 +2057,11 @@ def nest_runners(dev, nests: list[LoopNest]):
                 count = {"io": nin + 1, "io_scratch": nin + 1, "io_scratch_out": nin + 2}.get(launch.args, 2)
                 launchers.append((launch.args, _launcher(dev, functions[launch.name], launch, count - 1)))
             runners.append(_make_runner(dev, launchers, plan.scratch_bytes, extras, producer_inputs))
+        # the kernels this runner launches, by name (what a profile of the plan shows)
+        if role == "merged":
+            runners[-1].kernels = tuple(merged[key][1].name for key in prog.launches_from(k))
+        elif role == "launch":
+            runners[-1].kernels = tuple(launch.name for launch in plan.launches)
     return runners
 
 
