@@ -35,6 +35,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import re
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -1420,8 +1421,9 @@ def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set |
     MERGE_MEMBERS nests, MERGE_PARAMS pointers and MERGE_GROUP_GRID workgroups. An optimizer step
     gives groups across parameters: every parameter's moments in a first few groups, every
     parameter's update from its new moments in the next few, where a run of consecutive nests
-    took a launch per parameter. Nests in `taken` (members of row programs) never join.
-    `custom_inputs` None merges nothing."""
+    took a launch per parameter. Column reduces (a partials kernel and a fold kernel each) form
+    groups of their own kind: one launch of every member's partials, one of every fold. Nests in
+    `taken` (members of row programs) never join. `custom_inputs` None merges nothing."""
     if custom_inputs is None:
         return [], []
     fused = set(pairs) | set(pairs.values())
@@ -1433,6 +1435,7 @@ def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set |
         return nodes
 
     groups: list[list[int]] = []
+    kinds: list[str] = []  # "body" (single-launch nests) or "columns" (column reduces, two launches)
     size: list[list[int]] = []  # [workgroups, pointers] per group
     closed: list[bool] = []
     deps: list[set[int]] = []
@@ -1449,28 +1452,28 @@ def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set |
     for c, (nest, plan) in enumerate(zip(nests, plans)):
         if c in inlined.producers:
             continue  # launches nothing; its readers' reads() carry its inputs
-        ok = (
-            "body" in plan.notes
-            and c not in fused
-            and c not in taken
-            and len(plan.launches) == 1
-            and plan.launches[0].grid <= MERGE_GRID
-            and nest.kernel.target not in custom_inputs
-        )
+        free = c not in fused and c not in taken and nest.kernel.target not in custom_inputs
+        kind = None
+        if free and "body" in plan.notes and len(plan.launches) == 1 and plan.launches[0].grid <= MERGE_GRID:
+            kind = "body"
+        elif free and plan.notes.get("columns") and len(plan.launches) == 2:
+            kind = "columns"
         hit = {owner[n] for n in reads(c) if n in owner}
-        if not ok:
+        if kind is None:
             for g in hit:
                 close(g)
             continue
-        grid, params = plan.launches[0].grid, len(plan.notes["params"])
+        grid, params = plan.launches[0].grid, _param_count(plan) if kind == "columns" else len(plan.notes["params"])
         lo = max(hit) + 1 if hit else 0
-        target = next((g for g in range(lo, len(groups)) if not closed[g] and len(groups[g]) < MERGE_MEMBERS
-                       and size[g][0] + grid <= MERGE_GROUP_GRID and size[g][1] + params <= MERGE_PARAMS), None)
+        target = next((g for g in range(lo, len(groups)) if not closed[g] and kinds[g] == kind
+                       and len(groups[g]) < MERGE_MEMBERS and size[g][0] + grid <= MERGE_GROUP_GRID
+                       and size[g][1] + params <= MERGE_PARAMS), None)
         if target is None:
             groups.append([])
             size.append([0, 0])
             closed.append(False)
             deps.append(set())
+            kinds.append(kind)
             target = len(groups) - 1
         groups[target].append(c)
         size[target][0] += grid
@@ -1513,6 +1516,85 @@ def merged_source(name: str, nests: list[LoopNest], plans: list[Planned], run: l
     source = f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}({", ".join(params)}) {{\n' + "\n".join(segments) + "\n}"
     return source, offset
 
+
+
+_KERNEL_HEAD = re.compile(r'extern "C" __global__ __launch_bounds__\(\d+\) void (\w+)\((.*?)\) \{')
+
+
+_SHARED = re.compile(r"__shared__ (\w+) (\w+)((?:\[\d+\])+);")
+_SIZES = {"float": 4, "double": 8, "int": 4, "i64": 8, "short": 2, "char": 1}
+
+
+def as_device_function(source: str, grid: int) -> tuple[str, str, list[str], int]:
+    """A one-kernel source as a __device__ function of the same body that takes its workgroup
+    index as an argument (`mbid_`), its grid size a constant, and its LDS arrays from the caller's
+    `mshared_` (a workgroup runs one such function, so the functions of a merged kernel share
+    it): the function's name, its text, its parameter names in order and its LDS bytes."""
+    m = _KERNEL_HEAD.search(source)
+    assert m is not None, "not an emitted kernel"
+    name, params = m.group(1), m.group(2)
+    names = [p.split()[-1] for p in params.split(", ")]
+    body = source[m.end():].replace("blockIdx.x", "mbid_").replace("gridDim.x", f"{grid}")
+    at = 0
+
+    def shared(d) -> str:
+        nonlocal at
+        t, var, dims = d.group(1), d.group(2), [int(x) for x in re.findall(r"\d+", d.group(3))]
+        start = -(-at // 16) * 16
+        at = start + math.prod(dims) * _SIZES[t]
+        rest = "".join(f"[{x}]" for x in dims[1:])
+        return f"{t} (*{var}){rest} = ({t} (*){rest})(mshared_ + {start});" if rest else f"{t}* {var} = ({t}*)(mshared_ + {start});"
+
+    body = _SHARED.sub(shared, body)
+    text = f"__device__ __forceinline__ void {name}_d({params}, const i64 mbid_, char* mshared_) {{" + body
+    return f"{name}_d", text, names, at
+
+
+def _param_count(plan: Planned) -> int:
+    """The parameters of a plan's first kernel."""
+    return len(_KERNEL_HEAD.search(plan.source).group(2).split(", "))
+
+
+def _kernels_of(source: str) -> list[str]:
+    """The kernels of a plan's source, each from its `extern "C"` to the next."""
+    starts = [m.start() for m in _KERNEL_HEAD.finditer(source)]
+    return [source[a:b] for a, b in zip(starts, starts[1:] + [len(source)])]
+
+
+def merged_columns_source(name: str, plans: list[Planned], run: list[int]) -> tuple[str, int, int, list[int], int]:
+    """Two kernels for a group of column reduces: `<name>_part` runs every member's partials
+    kernel on its own range of workgroups, `<name>` every member's fold; each member's code is its
+    own kernel's, as a device function given its workgroup index. The members' partials share one
+    scratch buffer, at the returned byte offsets. Returns (source, partials grid, folds grid,
+    offsets, scratch bytes)."""
+    functions: list[str] = []
+    calls = {"part": [], "fold": []}
+    params = {"part": [], "fold": []}
+    grids = {"part": 0, "fold": 0}
+    lds = {"part": 0, "fold": 0}
+    offsets, total = [], 0
+    for s_, c in enumerate(run):
+        plan = plans[c]
+        offsets.append(total)
+        total += -(-plan.scratch_bytes // 256) * 256
+        part_src, fold_src = _kernels_of(plan.source)
+        for kind, src, launch in (("part", part_src, plan.launches[0]), ("fold", fold_src, plan.launches[1])):
+            fn, text, names, shared = as_device_function(src, launch.grid)
+            lds[kind] = max(lds[kind], shared)
+            functions.append(text)
+            m = _KERNEL_HEAD.search(src)
+            for decl, pname in zip(m.group(2).split(", "), names):
+                params[kind].append(decl[: len(decl) - len(pname)] + f"s{s_}_{pname}")
+            start = grids[kind]
+            grids[kind] += launch.grid
+            args = ", ".join(f"s{s_}_{pname}" for pname in names)
+            calls[kind].append(f"  if (b_ < {grids[kind]}) {{ {fn}({args}, b_ - {start}, mshared_); return; }}")
+    kernels = []
+    for kind, kname in (("part", f"{name}_part"), ("fold", name)):
+        kernels.append(f'extern "C" __global__ __launch_bounds__({THREADS}) void {kname}({", ".join(params[kind])}) {{\n'
+                       f"  __shared__ __attribute__((aligned(16))) char mshared_[{max(lds[kind], 16)}];\n"
+                       "  const i64 b_ = blockIdx.x;\n" + "\n".join(calls[kind]) + "\n}")
+    return "\n".join(functions + kernels), grids["part"], grids["fold"], offsets, max(total, 256)
 
 
 # ---- row programs ---------------------------------------------------------------------------
@@ -1944,6 +2026,9 @@ class Program:
     # the nest whose runner launches each merged run (keyed as `merged`); a run missing here
     # launches from its last member's
     launch_at: dict[int, int] = field(default_factory=dict)
+    # merged column reduces (keyed as `merged`, whose launch is the partials kernel): the fold
+    # launch, each member's byte offset in the shared scratch, and the scratch's size
+    columns: dict[int, tuple[Launch, list[int], int]] = field(default_factory=dict)
 
     def launcher_of(self, key: int) -> int:
         return self.launch_at.get(key, key)
@@ -2001,18 +2086,25 @@ def plan_program(nests: list[LoopNest], kept: set | None, custom_inputs: set | N
         merged_sources.append(source)
         merged[chain[-1]] = (chain, Launch(name, grid, THREADS, "merged"))
     runs_all = runs + chains
+    columns: dict[int, tuple[Launch, list[int], int]] = {}
     for run, at in zip(runs, run_launch):
         name = f"{nests[run[0]].name}_to_{nests[run[-1]].name}"
-        source, grid = merged_source(name, nests, plans, run)
+        if plans[run[0]].notes.get("columns"):
+            source, part_grid, fold_grid, offsets, scratch = merged_columns_source(name, plans, run)
+            merged[run[-1]] = (run, Launch(f"{name}_part", part_grid, THREADS, "columns"))
+            columns[run[-1]] = (Launch(name, fold_grid, THREADS, "columns"), offsets, scratch)
+        else:
+            source, grid = merged_source(name, nests, plans, run)
+            merged[run[-1]] = (run, Launch(name, grid, THREADS, "merged"))
         merged_sources.append(source)
-        merged[run[-1]] = (run, Launch(name, grid, THREADS, "merged"))
         launch_at[run[-1]] = at
     in_run = {c for run in runs_all for c in run}
     names = [launch.name for k, p in enumerate(plans) if k not in in_run for launch in p.launches]
     names += [launch.name for _, launch in merged.values()]
+    names += [fold.name for fold, _, _ in columns.values()]
     kept_sources = [p.source for k, p in enumerate(plans) if k not in in_run]
     source = PRELUDE + "\n".join(kept_sources + merged_sources) if names else ""
-    return Program(plans, pairs, inlined, merged, source, names, launch_at)
+    return Program(plans, pairs, inlined, merged, source, names, launch_at, columns)
 
 
 def nest_runners(dev, nests: list[LoopNest]):
@@ -2039,9 +2131,15 @@ def nest_runners(dev, nests: list[LoopNest]):
             launches = []
             for key in prog.launches_from(k):
                 run, launch = merged[key]
+                if key in prog.columns:
+                    fold, offsets, scratch = prog.columns[key]
+                    count = sum(_param_count(plans[c]) for c in run)
+                    launches.append((_launcher(dev, functions[launch.name], launch, count - 1), run,
+                                     (_launcher(dev, functions[fold.name], fold, 2 * len(run) - 1), offsets, scratch, [])))
+                    continue
                 count = sum(len(plans[c].notes["params"]) for c in run)
-                launches.append((_launcher(dev, functions[launch.name], launch, count - 1), run))
-            runners.append(_merged_runner(launches, nests, inlined, producer_inputs, deferred, k))
+                launches.append((_launcher(dev, functions[launch.name], launch, count - 1), run, None))
+            runners.append(_merged_runner(dev, launches, nests, inlined, producer_inputs, deferred, k))
         elif role == "deferred":
             runners.append(_defer_runner(deferred, k))
         elif role == "epilogue":
@@ -2059,7 +2157,8 @@ def nest_runners(dev, nests: list[LoopNest]):
             runners.append(_make_runner(dev, launchers, plan.scratch_bytes, extras, producer_inputs))
         # the kernels this runner launches, by name (what a profile of the plan shows)
         if role == "merged":
-            runners[-1].kernels = tuple(merged[key][1].name for key in prog.launches_from(k))
+            runners[-1].kernels = tuple(name for key in prog.launches_from(k)
+                                        for name in (merged[key][1].name,) + ((prog.columns[key][0].name,) if key in prog.columns else ()))
         elif role == "launch":
             runners[-1].kernels = tuple(launch.name for launch in plan.launches)
     return runners
@@ -2076,23 +2175,40 @@ def _defer_runner(deferred: dict, k: int):
     return run
 
 
-def _merged_runner(launches: list, nests: list[LoopNest], inlined: "InlineSet", producer_inputs: dict,
+def _merged_runner(dev, launches: list, nests: list[LoopNest], inlined: "InlineSet", producer_inputs: dict,
                    deferred: dict, k: int):
-    """The runner that launches merged runs, (launch, members) in order, nest k among their
-    members: one launch per run over every member's buffers, in parameter order (inputs, an
-    inlined producer's inputs, out)."""
-    extras = {c: inlined.extras(nests[c]) for _, members in launches for c in members}
+    """The runner that launches merged runs, (launch, members, columns) in order, nest k among
+    their members: one launch per run over every member's buffers, in parameter order (inputs,
+    an inlined producer's inputs, out). A run of column reduces (`columns` = (fold launch, scratch
+    offsets, scratch bytes, held scratch)) launches its partials with each member's inputs and its
+    share of the scratch, then its folds with each member's scratch share and out; the scratch
+    is allocated on the first run and kept."""
+    extras = {c: inlined.extras(nests[c]) for _, members, _ in launches for c in members}
 
     def run(inputs: list, outs: list) -> None:
         deferred[k] = (inputs, outs)
-        for launch, members in launches:
+        for launch, members, columns in launches:
             ptrs: list[int] = []
-            for c in members:
+            if columns is None:
+                for c in members:
+                    ins, outs_c = deferred.pop(c)
+                    ptrs += [b.ptr for b in ins]
+                    ptrs += [producer_inputs[j][m].ptr for j, m in extras[c]]
+                    ptrs.append(outs_c[0].ptr)
+                launch(ptrs)
+                continue
+            fold, offsets, scratch, held = columns
+            if not held:
+                held.append(dev._alloc(scratch))
+            folds: list[int] = []
+            for c, off in zip(members, offsets):
                 ins, outs_c = deferred.pop(c)
                 ptrs += [b.ptr for b in ins]
                 ptrs += [producer_inputs[j][m].ptr for j, m in extras[c]]
-                ptrs.append(outs_c[0].ptr)
+                ptrs.append(held[0].ptr + off)
+                folds += [held[0].ptr + off, outs_c[0].ptr]
             launch(ptrs)
+            fold(folds)
 
     return run
 
