@@ -31,7 +31,16 @@ namespace {
 
 constexpr int LANES = 4;                     // lanes per resident row and key group
 constexpr int THREADS = 256;                 // per workgroup
-constexpr int STREAM = 32;                   // streamed rows per LDS tile
+// Streamed rows per LDS tile: 32 KiB of each streamed matrix at compute width, from 16 to 128
+// rows. Short heads are bound by the staging (a tile's global loads, then two barriers), not by
+// the few dot products per row a tile carries: at f32 and 64 dims, 128-row tiles take a 256-key
+// causal pass in 2 stages instead of 8. A multiple of every SPLIT, so each lane group folds the
+// same keys in the same order whatever the tile.
+template <typename C, int MAXD>
+constexpr int stream_rows() {
+  constexpr int rows = 32768 / (MAXD * (int)sizeof(C));
+  return rows > 128 ? 128 : rows < 16 ? 16 : rows;
+}
 // resident rows per workgroup when each row's streamed rows are split among SPLIT groups of lanes
 template <int SPLIT>
 constexpr int rows_per_block() { return THREADS / (LANES * SPLIT); }
@@ -57,16 +66,35 @@ __device__ __forceinline__ C row_sum(C x) {
   return x;
 }
 
+// LDS row stride of a streamed tile: MAXD + LANES elements. With SPLIT lane groups each group
+// reads its own streamed row, lane u of a group dims u, u + 4, ...; at a stride of MAXD (a
+// multiple of the 64 banks) every group's row sat on the same four banks and a read was a
+// 16-way conflict, at MAXD + 4 words the 16 groups' rows start 4 banks apart.
+template <int MAXD>
+constexpr int row_stride() { return MAXD + LANES; }
+
 // Stage rows [r0, r0 + STREAM) of a (rows, width) matrix into LDS at compute width, zero past
-// `rows` and past `width`.
+// `rows` and past `width`. Every load of the thread first, into registers, then the LDS writes:
+// written as one loop, each element's load was waited for before its write, and the passes of a
+// short head spent their time on one memory latency per staged element.
 template <typename T, int MAXD>
-__device__ __forceinline__ void stage(typename T::Compute (*tile)[MAXD], const typename T::Storage* base, int64_t r0,
+__device__ __forceinline__ void stage(typename T::Compute (*tile)[row_stride<MAXD>()], const typename T::Storage* base, int64_t r0,
                                       int64_t rows, int width) {
   typedef typename T::Compute C;
-  for (int idx = threadIdx.x; idx < STREAM * MAXD; idx += THREADS) {
+  constexpr int STREAM = stream_rows<C, MAXD>(), N = STREAM * MAXD / THREADS;
+  static_assert(N * THREADS == STREAM * MAXD, "a tile is a whole number of elements per thread");
+  C vals[N];
+#pragma unroll
+  for (int n = 0; n < N; n++) {
+    const int idx = threadIdx.x + n * THREADS;
     const int lr = idx / MAXD, d = idx - lr * MAXD;
     const int64_t r = r0 + lr;
-    tile[lr][d] = (r < rows && d < width) ? T::load(base, r * width + d) : C(0);
+    vals[n] = (r < rows && d < width) ? T::load(base, r * width + d) : C(0);
+  }
+#pragma unroll
+  for (int n = 0; n < N; n++) {
+    const int idx = threadIdx.x + n * THREADS;
+    tile[idx / MAXD][idx % MAXD] = vals[n];
   }
 }
 
@@ -130,8 +158,9 @@ __global__ __launch_bounds__(THREADS) void sdpa_fwd_rows(const typename T::Stora
                                                          typename T::Compute scale) {
   typedef typename T::Compute C;
   constexpr int P = MAXD / LANES, ROWS = rows_per_block<SPLIT>();
-  __shared__ C Kt[STREAM][MAXD];
-  __shared__ C Vt[STREAM][MAXD];
+  constexpr int STREAM = stream_rows<C, MAXD>();
+  __shared__ C Kt[STREAM][row_stride<MAXD>()];
+  __shared__ C Vt[STREAM][row_stride<MAXD>()];
   __shared__ C Mt[STREAM];
   const int64_t chunks = (t_q + ROWS - 1) / ROWS;
   const int64_t b = blockIdx.x / chunks, chunk = blockIdx.x - b * chunks;
@@ -196,8 +225,9 @@ __global__ __launch_bounds__(THREADS) void sdpa_bwd_q_rows(
     int hd_v, int causal, typename T::Compute scale) {
   typedef typename T::Compute C;
   constexpr int P = MAXD / LANES, ROWS = rows_per_block<SPLIT>();
-  __shared__ C Kt[STREAM][MAXD];
-  __shared__ C Vt[STREAM][MAXD];
+  constexpr int STREAM = stream_rows<C, MAXD>();
+  __shared__ C Kt[STREAM][row_stride<MAXD>()];
+  __shared__ C Vt[STREAM][row_stride<MAXD>()];
   __shared__ C Mt[STREAM];
   const int64_t chunks = (t_q + ROWS - 1) / ROWS;
   const int64_t b = blockIdx.x / chunks, chunk = blockIdx.x - b * chunks;
@@ -249,8 +279,9 @@ __global__ __launch_bounds__(THREADS) void sdpa_bwd_kv_rows(
     typename T::Compute scale) {
   typedef typename T::Compute C;
   constexpr int P = MAXD / LANES, ROWS = rows_per_block<SPLIT>();
-  __shared__ C Qt[STREAM][MAXD];
-  __shared__ C Ot[STREAM][MAXD];
+  constexpr int STREAM = stream_rows<C, MAXD>();
+  __shared__ C Qt[STREAM][row_stride<MAXD>()];
+  __shared__ C Ot[STREAM][row_stride<MAXD>()];
   __shared__ C Lt[STREAM];
   __shared__ C Dt[STREAM];
   const int64_t chunks = (t_k + ROWS - 1) / ROWS;
