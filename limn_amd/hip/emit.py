@@ -941,13 +941,13 @@ def plan_reduce(nest: LoopNest, shape: NestShape, bufs: Buffers) -> Planned:
         return out
 
     waves = THREADS // 64
-    if group == 64 and chunks < 64:
-        # a short row: G lanes (the power of two covering its VEC-wide chunks) per cell, 64 / G
-        # cells per wave, so a wave's loads cover whole consecutive rows; a butterfly within each
-        # group of lanes folds the cell
-        G = 1
-        while G < chunks:
-            G *= 2
+    if group == 64 and chunks < 256:
+        # a short row: G lanes per cell, 64 / G cells per wave, so a wave's loads cover whole
+        # consecutive rows; a butterfly within each group of lanes folds the cell. Under 64
+        # VEC-wide chunks G is the power of two covering them (a chunk a lane); from 64 it is a
+        # quarter of that (four chunks a lane, four rows a wave for a 512-wide bf16 row: a wave a
+        # row left each wave one row's loads in flight and half the rows for a second round)
+        G = lane_group(chunks)
         per_wave = 64 // G
         lines = [signature(nest.name, nest, out_dtype, bufs) + " {", "  const i64 bid_ = blockIdx.x, nblk_ = gridDim.x;"]
         lines.append(f"  const int lane = threadIdx.x & 63, sub_ = lane % {G};")
@@ -1064,6 +1064,15 @@ def fold_parts(name: str, shape: NestShape, acc_t: str, out_dtype: DType, out_re
     lines.append(f"      {out_ref} = {store_expr(out_dtype, 'acc')};")
     lines += ["    }", "  }", "}"]
     return lines, max(1, min(-(-cells // waves), 1 << 20))
+
+
+def lane_group(chunks: int) -> int:
+    """Lanes per cell of a row reduce over `chunks` vector chunks, under 256 of them (see
+    plan_reduce's short rows)."""
+    G = 1
+    while G < chunks:
+        G *= 2
+    return G if chunks < 64 else G // 4
 
 
 COLUMN_TILE = 64  # cells per workgroup of a column reduce: one wave's lanes, one coalesced row piece
@@ -1663,7 +1672,7 @@ def row_member(nest: LoopNest, plan: Planned) -> RowMember | None:
     shape = read_nest(nest)
     if shape.fold is not None:
         group = plan.notes.get("group")
-        if group not in (THREADS, 64) or plan.notes.get("columns") or len(shape.inner) != 1:
+        if group not in (THREADS, 64, 32, 16, 8) or plan.notes.get("columns") or len(shape.inner) != 1:
             return None
         if shape.reduce_dtype not in (float32, bfloat16, float16):
             return None
@@ -1796,13 +1805,16 @@ def row_chains(nests: list[LoopNest], plans: list[Planned], custom_inputs: set |
 # Re-read from memory, the passes of an 8192-float row softmax then LayerNorm (32 KB a row,
 # thousands of rows in flight) missed the L2 and ran at 2.5 TB/s of algorithmic bytes; the row
 # is 32 values a thread of a 256-thread workgroup.
-ROW_CACHE_VALUES = 32
+ROW_CACHE_VALUES = 64
 
 
-def _row_read(instr: Instr, inputs: list, member: RowMember):
+def _row_read(instr: Instr, inputs: list, member: RowMember, bufs: Buffers):
     """The input node that a member's LOAD reads at the member's (row, cell), unmasked - index the
-    row's row-major position times the row length plus the cell - or None."""
+    row's row-major position times the row length plus the cell - or None. Not a load of an
+    inlined producer's output: that buffer is never written, the load evaluates the producer."""
     if instr.opcode is not Opcode.LOAD or not instr.arg[0].startswith("in") or member.col is None:
+        return None
+    if instr.arg[0] in bufs.inline:
         return None
     buf, index, valid = instr.arg
     node = inputs[int(buf[2:])]
@@ -1824,8 +1836,8 @@ def row_source(name: str, nests: list[LoopNest], plans: list[Planned], run: list
     group = next(m.group for _, m in members if m.kind == "reduce")
     rows = math.prod(members[0][1].rows)
     cols = next(m.col[1] for _, m in members if m.col is not None)
-    threads = THREADS if group == THREADS else 64
-    tid = "threadIdx.x" if group == THREADS else "lane_"
+    threads = group  # the lanes of a row: a workgroup, a wave or a group of a wave's lanes
+    tid = "threadIdx.x" if group == THREADS else "lane_" if group == 64 else "sub_"
     # each member's buffers and cells per thread step
     setup = []
     for c, m in members:
@@ -1842,7 +1854,7 @@ def row_source(name: str, nests: list[LoopNest], plans: list[Planned], run: list
     readers: dict = {}
     for s_, (c, m) in enumerate(members):
         for instr in _loads(m.shape.body):
-            node = _row_read(instr, nests[c].kernel.inputs, m)
+            node = _row_read(instr, nests[c].kernel.inputs, m, setup[s_][0])
             if node is not None and s_ not in readers.setdefault(node, []):
                 readers[node].append(s_)
     cache: dict = {}
@@ -1862,10 +1874,18 @@ def row_source(name: str, nests: list[LoopNest], plans: list[Planned], run: list
         lines.append(f"  __shared__ float rp_fold_[{THREADS // 64}];")
         lines.append(f"  for (i64 row_ = blockIdx.x; row_ < {rows}LL; row_ += gridDim.x) {{")
         grid = max(1, min(rows, 1 << 20))
-    else:
+    elif group == 64:
         per = THREADS // 64
         lines.append("  const int lane_ = threadIdx.x & 63;")
         lines.append(f"  for (i64 row_ = (i64)blockIdx.x * {per} + (threadIdx.x >> 6); row_ < {rows}LL; row_ += (i64)gridDim.x * {per}) {{")
+        grid = max(1, min(-(-rows // per), 1 << 20))
+    else:
+        # 64 / group rows a wave, one a group of lanes (the rows of a wave's groups may end
+        # apart: a group's butterfly reads its own lanes only)
+        per = THREADS // group
+        lines.append(f"  const int lane_ = threadIdx.x & 63, sub_ = lane_ % {group};")
+        lines.append(f"  for (i64 row_ = ((i64)blockIdx.x * {THREADS // 64} + (threadIdx.x >> 6)) * {64 // group} + lane_ / {group}; "
+                     f"row_ < {rows}LL; row_ += (i64)gridDim.x * {per}) {{")
         grid = max(1, min(-(-rows // per), 1 << 20))
     for node, (var, vec, passes, same) in cache.items():
         first = same[0]
@@ -1890,7 +1910,7 @@ def row_source(name: str, nests: list[LoopNest], plans: list[Planned], run: list
         if not hits:
             return [f"{indent}for (i64 c_ = {tid}; c_ < {chunks}LL; c_ += {threads}) {{"], False
         for instr in _loads(m.shape.body):
-            node = _row_read(instr, nests[c].kernel.inputs, m)
+            node = _row_read(instr, nests[c].kernel.inputs, m, bufs)
             if node in cache and s_ in cache[node][3]:
                 bufs.cached[instr.dest] = f"{cache[node][0]}[it_][j_]"
         passes = hits[0][1][2]
@@ -1939,7 +1959,13 @@ def row_source(name: str, nests: list[LoopNest], plans: list[Planned], run: list
             lines += ["        " + value_line(i, bufs) for i in shape.body]
             lines.append("        " + _fold(shape.fold, "acc", f"({acc_t}){shape.item}"))
             lines += ["        }", "      }"]
-            lines.append(f"      acc = {'wave_fold_add' if shape.fold is Op.ADD else 'wave_fold_max'}(acc);")
+            if group >= 64:
+                lines.append(f"      acc = {'wave_fold_add' if shape.fold is Op.ADD else 'wave_fold_max'}(acc);")
+            else:  # the butterfly of plan_reduce's lane groups
+                k = group // 2
+                while k > 0:
+                    lines.append(f"      acc = {'fadd' if shape.fold is Op.ADD else 'fmax_nan'}(acc, ({acc_t})__shfl_xor(acc, {k}));")
+                    k //= 2
             if group == THREADS:
                 lines.append("      if ((threadIdx.x & 63) == 0) rp_fold_[threadIdx.x >> 6] = acc;")
                 lines.append("      __syncthreads();")

@@ -294,8 +294,8 @@ def test_a_large_sink_streams_its_stores():
 def test_softmax_layernorm_is_one_row_program():
     """The five launching nests of a row softmax then LayerNorm (max, sum of exp, mean, sum of
     squares, the final pass) run as one row program; a workgroup per row at 4096-wide rows, a
-    wave per row at 512."""
-    for n, group in ((4096, emit.THREADS), (512, 64)):
+    wave per row at 2048, a group of 32 lanes per row (two rows a wave) at 512."""
+    for n, group in ((4096, emit.THREADS), (2048, 64), (512, 32)):
         nests, kept = lowered([softmax_layernorm(n)])
         prog = emit.plan_program(nests, kept, set())
         assert len(prog.names) == 1 and "_rows_" in prog.names[0]
@@ -331,3 +331,25 @@ def test_a_read_of_another_row_ends_the_row_program():
     target = realized(z.node)
     assert all(nests[c].kernel.target is not target for run in runs for c in run)
     assert any(len(run) == 2 for run in runs)  # max and sum still share a row program
+
+
+def test_a_row_program_never_caches_an_inlined_producer():
+    """A small producer evaluated where it is read (a materialized x * 2 + a broadcast row, as the
+    GPT's embedding sum) feeding a LayerNorm: its output buffer is never written, so the row
+    program evaluates it in place instead of loading the row into registers from that buffer."""
+    from limn_amd.seam import nn
+    x = Tensor(rng.standard_normal((64, 128)).astype(np.float32))
+    pos = Tensor(rng.standard_normal((128,)).astype(np.float32))
+    from limn_amd.gpt import materialized
+    nests, kept = lowered([nn.LayerNorm(128)(materialized(x * 2.0 + pos))])
+    prog = emit.plan_program(nests, kept, set())
+    rows = [(run, launch) for run, launch in prog.merged.values() if "_rows_" in launch.name]
+    assert rows, "the LayerNorm runs as a row program"
+    run, launch = rows[0]
+    inlined = {nests[j].kernel.target for j in prog.inlined.producers}
+    assert any(n in inlined for c in run for n in nests[c].kernel.inputs)
+    src = prog.source[prog.source.index(f"void {launch.name}("):]
+    for c_s, c in enumerate(run):
+        for k, node in enumerate(nests[c].kernel.inputs):
+            if node in inlined:  # no register row is filled from the producer's buffer
+                assert f"__builtin_assume_aligned(s{c_s}_in{k}, 16) + row_" not in src

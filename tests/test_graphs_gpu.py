@@ -735,7 +735,11 @@ ROW_CASES = {
     # odd width: one value per vector chunk, a wave per row
     "softmax_layernorm_odd": ((33, 777), lambda x: _softmax_layernorm(Tensor(x))),
     "layernorm_bf16": ((100, 512), _layernorm(bfloat16, (100, 512))),
+    # 16 lanes a row, four rows a wave; 103 rows leave a wave with rows past the end
+    "layernorm_bf16_ragged": ((103, 512), _layernorm(bfloat16, (103, 512))),
     "layernorm_f16_3d": ((4, 50, 256), _layernorm(float16, (4, 50, 256))),
+    # 160 chunks: four a lane over a whole wave
+    "softmax_layernorm_640": ((45, 640), lambda x: _softmax_layernorm(Tensor(x))),
 }
 
 
