@@ -76,6 +76,15 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 // groups of 4 or 8, 0.554 with 16.
 constexpr int HEAD_GROUP = 4;
 
+// Work units of the D = 64 passes per head: under causality a block and its mirror (the block
+// counted from the other end) make one unit, so every unit walks the same number of tiles. At
+// short sequences every workgroup is resident at once, and unpaired the longest blocks ran on
+// alone at the end while the shorter ones had finished.
+template <bool CAUSAL>
+__host__ __device__ constexpr int64_t paired_units(int64_t blocks) {
+  return CAUSAL ? (blocks + 1) / 2 : blocks;
+}
+
 __device__ __forceinline__ void head_and_block(int64_t batch, int64_t nblocks, int64_t& b, int64_t& blk) {
   if (gridDim.x % 8 == 0) {
     const int64_t id = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
@@ -278,9 +287,15 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
   // uniform branches instead of exec-masked ones
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
   const int64_t nqb = (t_q + ROWS - 1) / ROWS;
-  int64_t b, blk;
-  head_and_block(batch, nqb, b, blk);
-  const int64_t qb = nqb - 1 - blk;  // causal: the longest rows go first
+  // causal: a workgroup takes a block and its mirror, nqb - 1 - u then u, so that every
+  // workgroup has the same work (see paired_units)
+  const int64_t units = paired_units<CAUSAL>(nqb);
+  int64_t b, unit;
+  head_and_block(batch, units, b, unit);
+  const int reps = CAUSAL && nqb - 1 - unit != unit ? 2 : 1;
+#pragma unroll 1
+  for (int rep = 0; rep < reps; rep++) {
+  const int64_t qb = rep == 0 ? nqb - 1 - unit : unit;  // causal: the longest rows go first
   const int q0 = (int)qb * ROWS, wq0 = q0 + wave * 32 * NT;
   const Rows qrows(q + b * (int64_t)t_q * D, t_q, D);
   const Rows krows(k + b * (int64_t)t_k * D, t_k, D), vrows(v + b * (int64_t)t_k * D, t_k, D);
@@ -400,6 +415,8 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
     store_transposed<T, D>(out + b * (int64_t)t_q * D, acc[t], row, t_q, 1.f / total);
     if (h == 0 && row < t_q) lse[b * (int64_t)t_q + row] = m[t] * scale + logf(total);
   }
+    __syncthreads();  // the pair's second block reuses the LDS tiles
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -419,9 +436,15 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_bwd_q_mfma(cons
   // uniform branches instead of exec-masked ones
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
   const int64_t nqb = (t_q + ROWS - 1) / ROWS;
-  int64_t b, blk;
-  head_and_block(batch, nqb, b, blk);
-  const int64_t qb = nqb - 1 - blk;  // causal: the longest rows go first
+  // causal: a workgroup takes a block and its mirror, nqb - 1 - u then u, so that every
+  // workgroup has the same work (see paired_units)
+  const int64_t units = paired_units<CAUSAL>(nqb);
+  int64_t b, unit;
+  head_and_block(batch, units, b, unit);
+  const int reps = CAUSAL && nqb - 1 - unit != unit ? 2 : 1;
+#pragma unroll 1
+  for (int rep = 0; rep < reps; rep++) {
+  const int64_t qb = rep == 0 ? nqb - 1 - unit : unit;  // causal: the longest rows go first
   const int q0 = (int)qb * ROWS, wq0 = q0 + wave * 32 * NT;
   const Rows qrows(q + b * (int64_t)t_q * D, t_q, D), orows(dout + b * (int64_t)t_q * D, t_q, D);
   const Rows krows(k + b * (int64_t)t_k * D, t_k, D), vrows(v + b * (int64_t)t_k * D, t_k, D);
@@ -522,6 +545,8 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_bwd_q_mfma(cons
   }
 #pragma unroll
   for (int t = 0; t < NT; t++) store_transposed<T, D>(dq + b * (int64_t)t_q * D, acc[t], wq0 + 32 * t + n, t_q, 1.f);
+    __syncthreads();  // the pair's second block reuses the LDS tiles
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -543,8 +568,15 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_bwd_kv_mfma(con
   // the wave index in a scalar register: the per-wave tile bounds and causal tests below are then
   // uniform branches instead of exec-masked ones
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
-  int64_t b, kb;  // causal: the first keys are seen by the most queries
-  head_and_block(batch, (t_k + ROWS - 1) / ROWS, b, kb);
+  // causal: the first keys are seen by the most queries; a workgroup takes a key block and its
+  // mirror, u then nkb - 1 - u (see paired_units)
+  const int64_t nkb = (t_k + ROWS - 1) / ROWS, units = paired_units<CAUSAL>(nkb);
+  int64_t b, unit;
+  head_and_block(batch, units, b, unit);
+  const int reps = CAUSAL && nkb - 1 - unit != unit ? 2 : 1;
+#pragma unroll 1
+  for (int rep = 0; rep < reps; rep++) {
+  const int64_t kb = rep == 0 ? unit : nkb - 1 - unit;
   const int k0 = (int)kb * ROWS, wk0 = k0 + wave * 32 * NT;
   const Rows qrows(q + b * (int64_t)t_q * D, t_q, D), orows(dout + b * (int64_t)t_q * D, t_q, D);
   const Rows krows(k + b * (int64_t)t_k * D, t_k, D), vrows(v + b * (int64_t)t_k * D, t_k, D);
@@ -699,6 +731,8 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_bwd_kv_mfma(con
     const int key = wk0 + 32 * t + n;
     store_transposed<T, D>(dk + b * (int64_t)t_k * D, gk[t], key, t_k, 1.f);
     store_transposed<T, D>(dv + b * (int64_t)t_k * D, gv[t], key, t_k, 1.f);
+  }
+    __syncthreads();  // the pair's second block reuses the LDS tiles
   }
 }
 
@@ -1493,7 +1527,9 @@ int launch_nt(const SdpaArgs& a) {
   constexpr SdpaPass pass = PASS;
   const int64_t rows = pass == SDPA_BWD_KV ? a.t_k : a.t_q;
   const int64_t per = 128 * NT;
-  const int64_t blocks = a.batch * ((rows + per - 1) / per);
+  // the D = 128 kernels take a block each; the D = 64 ones a unit of paired blocks
+  const int64_t per_head = (rows + per - 1) / per;
+  const int64_t blocks = a.batch * (D == 128 ? per_head : paired_units<CAUSAL>(per_head));
   if (blocks > 0x7fffffff) return fail(LIMN_HIP_EUNSUPPORTED, "sdpa: %lld workgroups exceed one launch", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(THREADS);
   const float scale = (float)a.scale;
