@@ -691,6 +691,55 @@ def test_matmul_layouts_through_the_c_abi(hipdev, a_kcontig, b_kcontig, M, N, K,
         np.testing.assert_allclose(got, exact, rtol=2**-7, atol=1e-2 * np.sqrt(K / 1024))
 
 
+@pytest.mark.parametrize(
+    "M,N,K,b_kcontig,layout",
+    [
+        (4160, 4096, 64, True, "rows"),
+        (4160, 4096, 64, True, "rows+4"),
+        (4160, 4096, 64, True, "rows+1"),
+        (4160, 4100, 64, True, "rows"),
+        (4160, 4096, 64, False, "columns"),
+        (200, 72, 1024, False, "columns"),
+        (304, 262, 8192, True, "rows"),
+        (304, 264, 8192, False, "rows+4"),
+    ],
+    ids=str,
+)
+def test_matmul_output_layouts_through_the_c_abi(hipdev, M, N, K, b_kcontig, layout):
+    """The store paths of the staged epilogue: 16-byte row stores ("rows", a 256-tile at 4160 x
+    4096), 8-byte ones (an output 8 bytes past a 16-byte boundary, or rows of 4100), element
+    stores (an odd element offset, a transposed output), row tails (N = 4100, 262), and the
+    float32 partials of a split k with N % 4 != 0. Cells outside the output must stay as they
+    were. Against the float64 product of the same bf16 values, rounded once."""
+    from limn_amd.dtypes import bf16_bits, bf16_values
+    from limn_amd.hip import runtime
+
+    a_vals = bf16_values(bf16_bits(rng.standard_normal((M, K)).astype(np.float32)))
+    b_vals = bf16_values(bf16_bits(rng.standard_normal((K, N)).astype(np.float32)))
+    b_store = np.ascontiguousarray(b_vals.T) if b_kcontig else b_vals
+    b_k, b_n = (1, K) if b_kcontig else (N, 1)
+    lib = runtime.kernels()
+    a, b = hipdev.alloc(a_vals.size * 2), hipdev.alloc(b_store.size * 2)
+    hipdev.copyin(a, bf16_bits(a_vals))
+    hipdev.copyin(b, bf16_bits(b_store))
+    ws_bytes = lib.limn_hip_matmul_workspace(3, 1, M, N, K)
+    ws = hipdev.alloc(ws_bytes) if ws_bytes else None
+    offset = {"rows": 0, "rows+4": 4, "rows+1": 1, "columns": 0}[layout]
+    c_m, c_n = (1, M) if layout == "columns" else (N, 1)
+    sentinel = np.full(M * N + 16, 0x7FC1, np.uint16)  # a NaN no product rounds to
+    c = hipdev.alloc(sentinel.size * 2)
+    hipdev.copyin(c, sentinel)
+    runtime.check_limn(lib.limn_hip_matmul(a.ptr, b.ptr, c.ptr + 2 * offset, 3, 1, M, N, K, 0, K, 1, 0, b_k, b_n, 0, c_m,
+                                           c_n, 0, None if ws is None else ws.ptr, ws_bytes, None))
+    hipdev.finish()
+    raw = hipdev.copyout(c).view(np.uint16)
+    assert (raw[:offset] == 0x7FC1).all() and (raw[offset + M * N:] == 0x7FC1).all(), "a store left the output"
+    cells = raw[offset:offset + M * N]
+    got = bf16_values(cells.reshape(N, M).T if layout == "columns" else cells.reshape(M, N)).astype(np.float64)
+    exact = a_vals.astype(np.float64) @ b_vals.astype(np.float64)
+    np.testing.assert_allclose(got, exact, rtol=2**-7, atol=1e-2 * np.sqrt(K / 1024))
+
+
 @pytest.mark.parametrize("shape,dtype", [((8, 512, 96), float32), ((4, 300, 1536), bfloat16), ((2, 64, 200), float32)], ids=str)
 def test_column_reduce_over_batch_and_rows(hipdev, shape, dtype):
     """A bias gradient's shape: (b, t, c) summed over b and t. 64 cells per workgroup, rows
