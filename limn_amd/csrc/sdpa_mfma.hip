@@ -236,6 +236,34 @@ __device__ __forceinline__ void store_transposed(u16* base, const f32x16* acc, i
   }
 }
 
+// The wave's 32 rows x D dims of an accumulator set (lane n = row, items = dims, the layout
+// store_transposed takes) to global rows [row0, row0 + 32) of a (rows x D) matrix, scaled by
+// `mul`, through an LDS stage of 32 rows padded by 16 bytes: D / 8 8-byte LDS writes per lane,
+// then 16-byte global stores each covering 512 / D whole rows. store_transposed's 8-byte stores
+// touch 32 rows per instruction; staged, the D = 128 dK/dV pass took 1.143 ms against 1.194.
+// The wave reads only what it wrote itself, so no barrier is needed between the two halves.
+template <typename T, int D>
+__device__ __forceinline__ void store_staged(u16* base, const f32x16* acc, int row0, int rows, float mul, u16* stage) {
+  const int lane = threadIdx.x & 63, h = lane >> 5, n = lane & 31;
+  constexpr int RS = D + 8;      // padded row stride, elements
+  constexpr int CPR = D / 8;     // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;  // rows one store instruction covers
+#pragma unroll
+  for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const u16x4 o = {T::pack(acc[dt][4 * g] * mul), T::pack(acc[dt][4 * g + 1] * mul), T::pack(acc[dt][4 * g + 2] * mul),
+                       T::pack(acc[dt][4 * g + 3] * mul)};
+      *(u16x4*)(stage + n * RS + dt * 32 + 8 * g + 4 * h) = o;
+    }
+#pragma unroll
+  for (int j = 0; j < 32 / RPI; j++) {
+    const int r = RPI * j + lane / CPR, c = lane % CPR;
+    const u16x8 v = *(const u16x8*)(stage + r * RS + c * 8);
+    if (row0 + r < rows) *(u16x8*)(base + (int64_t)(row0 + r) * D + c * 8) = v;
+  }
+}
+
 // One batch row of the key mask, read through a buffer resource: entries past t_k read as zero,
 // which is "hidden", so the last tile needs no bounds test.
 struct MaskRow {
@@ -408,11 +436,13 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_fwd_mfma(const 
     }
     __syncthreads();
   }
+  __syncthreads();  // every wave is done with the tiles: each stages its output in one
+  u16* stage = wave == 0 ? Ks[0] : wave == 1 ? Ks[1] : wave == 2 ? Vs[0] : Vs[1];
 #pragma unroll
   for (int t = 0; t < NT; t++) {
     const int row = wq0 + 32 * t + n;
     const float total = pair_sum(l[t]);
-    store_transposed<T, D>(out + b * (int64_t)t_q * D, acc[t], row, t_q, 1.f / total);
+    store_staged<T, D>(out + b * (int64_t)t_q * D, acc[t], wq0 + 32 * t, t_q, 1.f / total, stage);
     if (h == 0 && row < t_q) lse[b * (int64_t)t_q + row] = m[t] * scale + logf(total);
   }
     __syncthreads();  // the pair's second block reuses the LDS tiles
@@ -543,8 +573,10 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_bwd_q_mfma(cons
     }
     __syncthreads();
   }
+  __syncthreads();  // every wave is done with the tiles: each stages its output in one
+  u16* stage = wave == 0 ? Ks[0] : wave == 1 ? Ks[1] : wave == 2 ? Vs[0] : Vs[1];
 #pragma unroll
-  for (int t = 0; t < NT; t++) store_transposed<T, D>(dq + b * (int64_t)t_q * D, acc[t], wq0 + 32 * t + n, t_q, 1.f);
+  for (int t = 0; t < NT; t++) store_staged<T, D>(dq + b * (int64_t)t_q * D, acc[t], wq0 + 32 * t, t_q, 1.f, stage);
     __syncthreads();  // the pair's second block reuses the LDS tiles
   }
 }
@@ -726,11 +758,12 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_bwd_kv_mfma(con
     }
     __syncthreads();
   }
+  __syncthreads();  // every wave is done with the tiles: each stages its output in one
+  u16* stage = wave == 0 ? Qs[0] : wave == 1 ? Qs[1] : wave == 2 ? Os[0] : Os[1];
 #pragma unroll
   for (int t = 0; t < NT; t++) {
-    const int key = wk0 + 32 * t + n;
-    store_transposed<T, D>(dk + b * (int64_t)t_k * D, gk[t], key, t_k, 1.f);
-    store_transposed<T, D>(dv + b * (int64_t)t_k * D, gv[t], key, t_k, 1.f);
+    store_staged<T, D>(dk + b * (int64_t)t_k * D, gk[t], wk0 + 32 * t, t_k, 1.f, stage);
+    store_staged<T, D>(dv + b * (int64_t)t_k * D, gv[t], wk0 + 32 * t, t_k, 1.f, stage);
   }
     __syncthreads();  // the pair's second block reuses the LDS tiles
   }
@@ -1005,31 +1038,6 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_dma(const u16* __restr
 // removed runs at 1350 TFLOP/s (the MFMAs alone at 2100), and one wave per SIMD hides only a few
 // VALU instructions per MFMA of its own, which is what bounds both kernels.
 
-// the wave's 32 rows x 128 dims of an accumulator set (lane n = row, items = dims, the layout
-// store_transposed takes) to global rows [row0, row0 + 32) of a (rows x 128) matrix through an
-// LDS stage of 32 rows padded to 272 bytes: 16 8-byte LDS writes per lane, then 8 16-byte global
-// stores per lane covering 4 whole rows each. store_transposed's 8-byte stores touch 32 rows per
-// instruction; staged, the dK/dV pass above took 1.143 ms against 1.194.
-template <typename T>
-__device__ __forceinline__ void store_staged(u16* base, const f32x16* acc, int row0, int rows, float mul, u16* stage) {
-  const int lane = threadIdx.x & 63, h = lane >> 5, n = lane & 31;
-  constexpr int RS = 136;  // padded row stride, elements
-#pragma unroll
-  for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-      const u16x4 o = {T::pack(acc[dt][4 * g] * mul), T::pack(acc[dt][4 * g + 1] * mul), T::pack(acc[dt][4 * g + 2] * mul),
-                       T::pack(acc[dt][4 * g + 3] * mul)};
-      *(u16x4*)(stage + n * RS + dt * 32 + 8 * g + 4 * h) = o;
-    }
-#pragma unroll
-  for (int j = 0; j < 8; j++) {
-    const int r = 4 * j + (lane >> 4), c = lane & 15;
-    const u16x8 v = *(const u16x8*)(stage + r * RS + c * 8);
-    if (row0 + r < rows) *(u16x8*)(base + (int64_t)(row0 + r) * 128 + c * 8) = v;
-  }
-}
-
 template <typename T, bool CAUSAL>
 __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_piped(const u16* __restrict__ q, const u16* __restrict__ k,
                                                                 const u16* __restrict__ v, const u16* __restrict__ dout,
@@ -1234,8 +1242,8 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_piped(const u16* __res
   __builtin_amdgcn_s_waitcnt(WAIT_VMEM);  // the copies issued for tiles past the end
   __syncthreads();                        // every wave is done with the tile buffers
   u16* stage = wave == 0 ? Q0 : wave == 1 ? Q1 : wave == 2 ? O0 : O1;
-  store_staged<T>(dk + b * (int64_t)t_k * D, gk, wk0, t_k, 1.f, stage);
-  store_staged<T>(dv + b * (int64_t)t_k * D, gv, wk0, t_k, 1.f, stage);
+  store_staged<T, 128>(dk + b * (int64_t)t_k * D, gk, wk0, t_k, 1.f, stage);
+  store_staged<T, 128>(dv + b * (int64_t)t_k * D, gv, wk0, t_k, 1.f, stage);
 }
 
 // ---- forward at D = 128: streamed K and V tiles copied straight into LDS ------------------------
@@ -1374,7 +1382,7 @@ __global__ __launch_bounds__(THREADS, 2) void sdpa_fwd_dma(const u16* __restrict
   const float total = pair_sum(l);
   // the tile buffers are free: the last step waited for its copy and passed the barrier
   u16* stage = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? V0 : V1;
-  store_staged<T>(out + b * (int64_t)t_q * D, acc, q0 + wave * 32, t_q, 1.f / total, stage);
+  store_staged<T, 128>(out + b * (int64_t)t_q * D, acc, q0 + wave * 32, t_q, 1.f / total, stage);
   if (h == 0 && row < t_q) lse[b * (int64_t)t_q + row] = m * scale + logf(total);
 }
 
@@ -1507,7 +1515,7 @@ __global__ __launch_bounds__(THREADS, 2) void sdpa_bwd_q_dma(const u16* __restri
   run(std::false_type{}, 0, open);
   run(std::true_type{}, open, ntiles);
   u16* stage = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? V0 : V1;  // free after the last barrier
-  store_staged<T>(dq + b * (int64_t)t_q * D, acc, q0 + wave * 32, t_q, 1.f, stage);
+  store_staged<T, 128>(dq + b * (int64_t)t_q * D, acc, q0 + wave * 32, t_q, 1.f, stage);
 }
 
 // ---------------------------------------------------------------------------------------------
