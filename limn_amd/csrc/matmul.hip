@@ -52,6 +52,50 @@ __device__ __forceinline__ u16x8 zero8() {
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
+// The addends of one output cell: t is the contraction already rounded to T.
+template <typename T>
+__device__ __forceinline__ u16 add_terms(u16 t, const MatmulAddends& add, int64_t bz, int64_t row, int64_t col) {
+  float x = T::unpack(t);
+  if (add.bias != nullptr) x = x + T::unpack(add.bias[col * add.bias_n]);
+  if (add.res != nullptr) x = T::unpack(add.res[bz * add.r_batch + row * add.r_m + col * add.r_n]) + x;
+  return T::pack(x);
+}
+
+// The bias of 8 consecutive n, and the residual of 8 consecutive n of one row: 16-byte loads where
+// the terms are contiguous and aligned and the 8 cells lie before N (col is a multiple of 8), else
+// element loads; cells past N read zeros (they are not stored).
+__device__ __forceinline__ u16x8 bias8(const MatmulAddends& add, int64_t col, int64_t N) {
+  u16x8 v = zero8();
+  if (add.bias == nullptr) return v;
+  if ((add.vec & 1) && col + 7 < N) return *(const u16x8*)(add.bias + col);
+#pragma unroll
+  for (int e = 0; e < 8; e++) v[e] = col + e < N ? add.bias[(col + e) * add.bias_n] : (u16)0;
+  return v;
+}
+__device__ __forceinline__ u16x8 res8(const MatmulAddends& add, int64_t bz, int64_t row, int64_t col, int64_t N) {
+  u16x8 v = zero8();
+  if (add.res == nullptr) return v;
+  const u16* r = add.res + bz * add.r_batch + row * add.r_m;
+  if ((add.vec & 2) && col + 7 < N) return *(const u16x8*)(r + col);
+#pragma unroll
+  for (int e = 0; e < 8; e++) v[e] = col + e < N ? r[(col + e) * add.r_n] : (u16)0;
+  return v;
+}
+
+// 8 rounded contraction cells (packed two to a word) with their terms added, rounded again.
+template <typename T>
+__device__ __forceinline__ u32x4 add_terms8(u32x4 w, u16x8 bv, u16x8 rv, const MatmulAddends& add) {
+  u16x8 t = __builtin_bit_cast(u16x8, w);
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    float x = T::unpack(t[e]);
+    if (add.bias != nullptr) x = x + T::unpack(bv[e]);
+    if (add.res != nullptr) x = T::unpack(rv[e]) + x;
+    t[e] = T::pack(x);
+  }
+  return __builtin_bit_cast(u32x4, t);
+}
+
 // One operand's LDS tile per stage, kept in its memory orientation:
 //   k-contiguous operand -> [ROWS][BK + 8]: an MFMA operand is one ds_read_b128 of a row (the
 //     row stride is 9 sixteen-byte groups, so the 16 rows a read serves per cycle hit 16 groups);
@@ -119,7 +163,7 @@ struct Operand {
 template <typename T, int BM, int BN, bool A_K, bool B_K, int EPI, bool PARTIAL>
 __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restrict__ a, const u16* __restrict__ b,
                                                              u16* __restrict__ c, float* __restrict__ ws, MatmulShape s,
-                                                             int64_t chunk) {
+                                                             int64_t chunk, MatmulAddends add) {
   constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 accumulators per wave along m and n
   using OA = Operand<BM, A_K>;
   using OB = Operand<BN, B_K>;
@@ -213,7 +257,9 @@ __global__ __launch_bounds__(MM_THREADS, 1) void matmul_mfma(const u16* __restri
         if (row < s.M) {
           float v = acc[i][j][e];
           if (EPI == MATMUL_EPILOGUE_RELU) v = v > 0.f ? v : 0.f;
-          cbase[row * s.c_m + col * s.c_n] = T::pack(v);
+          u16 t = T::pack(v);
+          if (add.bias != nullptr || add.res != nullptr) t = add_terms<T>(t, add, bz, row, col);
+          cbase[row * s.c_m + col * s.c_n] = t;
         }
       }
     }
@@ -308,7 +354,8 @@ struct DmaTile {
 template <typename T, int BM, int BN, bool A_K, bool B_K, int EPI, bool PARTIAL>
 __global__ __launch_bounds__(64 * DmaTile<BM>::WAVES, 2) void matmul_dma(const u16* __restrict__ a, const u16* __restrict__ b,
                                                                       u16* __restrict__ c, float* __restrict__ ws,
-                                                                      MatmulShape s, int64_t chunk, int wide) {
+                                                                      MatmulShape s, int64_t chunk, int wide,
+                                                                      MatmulAddends add) {
   constexpr int WAVES = DmaTile<BM>::WAVES, WN = DmaTile<BM>::WN;
   constexpr int WTM = BM / 2, WTN = BN / WN;  // one wave's output tile
   constexpr int TM = WTM / 32, TN = WTN / 32, KS = BK / 16;
@@ -449,13 +496,29 @@ __global__ __launch_bounds__(64 * DmaTile<BM>::WAVES, 2) void matmul_dma(const u
         }
     }
     const int cc = lane % CPR;
+    constexpr int ITS = IB * 32 / RPI;
+    // the added terms first, every load in flight before the first store (as far as the compiler
+    // knows the stores may alias them, so a load after a store would wait for it): the bias chunk
+    // is the same for every row a lane stores, the residual one chunk per row
+    const bool adds = !PARTIAL && (add.bias != nullptr || add.res != nullptr);
+    u16x8 bv = zero8(), rv[ITS];
+    if (adds) {
+      const int64_t col = n0 + wn * WTN + cc * 8;
+      bv = bias8(add, col, s.N);
 #pragma unroll
-    for (int it = 0; it < IB * 32 / RPI; it++) {
+      for (int it = 0; it < ITS; it++) {
+        const int64_t row = m0 + wm * WTM + p * IB * 32 + it * RPI + lane / CPR;
+        rv[it] = row < s.M && col < s.N ? res8(add, bz, row, col, s.N) : zero8();
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < ITS; it++) {
       const int r = it * RPI + lane / CPR;
-      const u32x4 w = *(const u32x4*)(region + r * RB + (cc ^ swz(r)) * 16);
+      const u32x4 staged = *(const u32x4*)(region + r * RB + (cc ^ swz(r)) * 16);
       const int64_t row = m0 + wm * WTM + p * IB * 32 + r, col = n0 + wn * WTN + cc * (16 / ES);
       if (row >= s.M || col >= s.N) continue;
       if (PARTIAL) {
+        const u32x4 w = staged;
         float* wp = ws + (slice * s.batch + bz) * s.M * s.N + row * s.N + col;
         if (wide && col + 3 < s.N) {
           *(u32x4*)wp = w;
@@ -466,6 +529,7 @@ __global__ __launch_bounds__(64 * DmaTile<BM>::WAVES, 2) void matmul_dma(const u
         }
       } else {
         u16* o = c + bz * s.c_batch + row * s.c_m + col * s.c_n;
+        const u32x4 w = adds ? add_terms8<T>(staged, bv, rv[it], add) : staged;
         if (wide == 2 && col + 7 < s.N) {
           *(u32x4*)o = w;
         } else if (wide && col + 7 < s.N) {
@@ -487,7 +551,7 @@ __global__ __launch_bounds__(64 * DmaTile<BM>::WAVES, 2) void matmul_dma(const u
 #define LIMN_DMA_INSTANCE(T, BM, AK, BKC, EPI, P)                                                               \
   template __global__ void matmul_dma<T, BM, BM, AK, BKC, EPI, P>(const u16* __restrict__, const u16* __restrict__, \
                                                                   u16* __restrict__, float* __restrict__, MatmulShape, \
-                                                                  int64_t, int);
+                                                                  int64_t, int, MatmulAddends);
 #define LIMN_DMA_PARTIAL(T, BM, AK, BKC, EPI) LIMN_DMA_INSTANCE(T, BM, AK, BKC, EPI, false) LIMN_DMA_INSTANCE(T, BM, AK, BKC, EPI, true)
 #define LIMN_DMA_EPILOGUE(T, BM, AK, BKC) \
   LIMN_DMA_PARTIAL(T, BM, AK, BKC, MATMUL_EPILOGUE_NONE) LIMN_DMA_PARTIAL(T, BM, AK, BKC, MATMUL_EPILOGUE_RELU)
@@ -507,7 +571,8 @@ LIMN_DMA_LAYOUT(F16, 128)
 // store at c's strides.
 template <typename T, int EPI>
 __global__ __launch_bounds__(256) void matmul_splits(const float* __restrict__ ws, u16* __restrict__ c, MatmulShape s,
-                                                     int64_t split, int quad) {
+                                                     int64_t split, int quad, MatmulAddends add) {
+  const bool adds = add.bias != nullptr || add.res != nullptr;
   const int64_t total = s.batch * s.M * s.N;
   if (quad) {
     // 4 consecutive n per thread (N % 4 == 0, output rows contiguous and 8-byte aligned): one
@@ -529,8 +594,12 @@ __global__ __launch_bounds__(256) void matmul_splits(const float* __restrict__ w
         v.w = v.w > 0.f ? v.w : 0.f;
       }
       const int64_t col = i % s.N, row = (i / s.N) % s.M, bz = i / (s.N * s.M);
-      const uint2 packed = {(unsigned)T::pack(v.x) | ((unsigned)T::pack(v.y) << 16),
-                            (unsigned)T::pack(v.z) | ((unsigned)T::pack(v.w) << 16)};
+      u16 t[4] = {T::pack(v.x), T::pack(v.y), T::pack(v.z), T::pack(v.w)};
+      if (adds) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) t[e] = add_terms<T>(t[e], add, bz, row, col + e);
+      }
+      const uint2 packed = {(unsigned)t[0] | ((unsigned)t[1] << 16), (unsigned)t[2] | ((unsigned)t[3] << 16)};
       *(uint2*)(c + bz * s.c_batch + row * s.c_m + col) = packed;
     }
     return;
@@ -540,13 +609,14 @@ __global__ __launch_bounds__(256) void matmul_splits(const float* __restrict__ w
     for (int64_t k = 1; k < split; k++) v += ws[k * total + i];
     if (EPI == MATMUL_EPILOGUE_RELU) v = v > 0.f ? v : 0.f;
     const int64_t col = i % s.N, row = (i / s.N) % s.M, bz = i / (s.N * s.M);
-    c[bz * s.c_batch + row * s.c_m + col * s.c_n] = T::pack(v);
+    const u16 t = T::pack(v);
+    c[bz * s.c_batch + row * s.c_m + col * s.c_n] = adds ? add_terms<T>(t, add, bz, row, col) : t;
   }
 }
 
 template <typename T, int BM, int BN, bool A_K, bool B_K, int EPI>
-int launch_tile(const void* a, const void* b, void* c, const MatmulShape& s, const MatmulPlan& plan, void* ws,
-                hipStream_t stream) {
+int launch_tile(const void* a, const void* b, void* c, const MatmulShape& s, const MatmulPlan& plan,
+                const MatmulAddends& add, void* ws, hipStream_t stream) {
   const int64_t blocks = plan.split * s.batch * ((s.M + BM - 1) / BM) * ((s.N + BN - 1) / BN);
   if (blocks > 0x7fffffff) return fail(LIMN_HIP_EUNSUPPORTED, "matmul: %lld workgroups exceed one launch", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(MM_THREADS);
@@ -560,18 +630,18 @@ int launch_tile(const void* a, const void* b, void* c, const MatmulShape& s, con
     const dim3 dma_block(64 * DmaTile<BM>::WAVES);
     if (plan.split == 1) {
       hipLaunchKernelGGL((matmul_dma<T, BM, BN, A_K, B_K, EPI, false>), grid, dma_block, 0, stream, (const u16*)a,
-                         (const u16*)b, (u16*)c, (float*)nullptr, s, plan.chunk, wide);
+                         (const u16*)b, (u16*)c, (float*)nullptr, s, plan.chunk, wide, add);
       return check_hip(hipGetLastError(), "launching the matmul kernel");
     }
     hipLaunchKernelGGL((matmul_dma<T, BM, BN, A_K, B_K, EPI, true>), grid, dma_block, 0, stream, (const u16*)a,
-                       (const u16*)b, (u16*)c, (float*)ws, s, plan.chunk, wide);
+                       (const u16*)b, (u16*)c, (float*)ws, s, plan.chunk, wide, add);
   } else if (plan.split == 1) {
     hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, false>), grid, block, 0, stream, (const u16*)a,
-                       (const u16*)b, (u16*)c, (float*)nullptr, s, plan.chunk);
+                       (const u16*)b, (u16*)c, (float*)nullptr, s, plan.chunk, add);
     return check_hip(hipGetLastError(), "launching the matmul kernel");
   } else {
     hipLaunchKernelGGL((matmul_mfma<T, BM, BN, A_K, B_K, EPI, true>), grid, block, 0, stream, (const u16*)a,
-                       (const u16*)b, (u16*)c, (float*)ws, s, plan.chunk);
+                       (const u16*)b, (u16*)c, (float*)ws, s, plan.chunk, add);
   }
   const int rc = check_hip(hipGetLastError(), "launching the split matmul kernel");
   if (rc != LIMN_HIP_OK) return rc;
@@ -580,25 +650,25 @@ int launch_tile(const void* a, const void* b, void* c, const MatmulShape& s, con
   const int64_t per_thread = quad ? 4 : 1, threads = (total + per_thread - 1) / per_thread;
   const int64_t fold_blocks = (threads + 255) / 256 < 4096 ? (threads + 255) / 256 : 4096;
   hipLaunchKernelGGL((matmul_splits<T, EPI>), dim3((unsigned)fold_blocks), dim3(256), 0, stream, (const float*)ws,
-                     (u16*)c, s, plan.split, (int)quad);
+                     (u16*)c, s, plan.split, (int)quad, add);
   return check_hip(hipGetLastError(), "launching the matmul slice fold");
 }
 
 template <typename T, bool A_K, bool B_K, int EPI>
-int launch_layout(const void* a, const void* b, void* c, const MatmulShape& s, const MatmulPlan& plan, void* ws,
-                  hipStream_t stream) {
-  if (plan.tile == 256) return launch_tile<T, 256, 256, A_K, B_K, EPI>(a, b, c, s, plan, ws, stream);
-  return launch_tile<T, 128, 128, A_K, B_K, EPI>(a, b, c, s, plan, ws, stream);
+int launch_layout(const void* a, const void* b, void* c, const MatmulShape& s, const MatmulPlan& plan,
+                  const MatmulAddends& add, void* ws, hipStream_t stream) {
+  if (plan.tile == 256) return launch_tile<T, 256, 256, A_K, B_K, EPI>(a, b, c, s, plan, add, ws, stream);
+  return launch_tile<T, 128, 128, A_K, B_K, EPI>(a, b, c, s, plan, add, ws, stream);
 }
 
 template <typename T, int EPI>
-int launch_type(const void* a, const void* b, void* c, const MatmulShape& s, const MatmulPlan& plan, void* ws,
-                hipStream_t stream) {
+int launch_type(const void* a, const void* b, void* c, const MatmulShape& s, const MatmulPlan& plan,
+                const MatmulAddends& add, void* ws, hipStream_t stream) {
   const bool a_k = s.a_k == 1, b_k = s.b_k == 1;
-  if (a_k && b_k) return launch_layout<T, true, true, EPI>(a, b, c, s, plan, ws, stream);
-  if (a_k) return launch_layout<T, true, false, EPI>(a, b, c, s, plan, ws, stream);
-  if (b_k) return launch_layout<T, false, true, EPI>(a, b, c, s, plan, ws, stream);
-  return launch_layout<T, false, false, EPI>(a, b, c, s, plan, ws, stream);
+  if (a_k && b_k) return launch_layout<T, true, true, EPI>(a, b, c, s, plan, add, ws, stream);
+  if (a_k) return launch_layout<T, true, false, EPI>(a, b, c, s, plan, add, ws, stream);
+  if (b_k) return launch_layout<T, false, true, EPI>(a, b, c, s, plan, add, ws, stream);
+  return launch_layout<T, false, false, EPI>(a, b, c, s, plan, add, ws, stream);
 }
 
 constexpr int64_t FILL = 256;        // workgroups that give every CU one (one workgroup per CU fits)
@@ -654,17 +724,17 @@ int64_t matmul_workspace_bytes(const MatmulShape& s) {
   return plan.split > 1 ? plan.split * s.batch * s.M * s.N * (int64_t)sizeof(float) : 0;
 }
 
-int launch_matmul(const void* a, const void* b, void* c, int dtype, const MatmulShape& s, int epilogue, void* workspace,
-                  int64_t workspace_bytes, hipStream_t stream) {
+int launch_matmul(const void* a, const void* b, void* c, int dtype, const MatmulShape& s, int epilogue,
+                  const MatmulAddends& add, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   MatmulPlan plan = plan_matmul(s);
   if (plan.split > 1 && (workspace == nullptr || workspace_bytes < matmul_workspace_bytes(s)))
     plan = {plan.tile, 1, s.K};  // no room for the slices: the same contraction, unsplit
   const bool relu = epilogue == MATMUL_EPILOGUE_RELU;
   if (dtype == LIMN_HIP_BFLOAT16)
-    return relu ? launch_type<BF16, MATMUL_EPILOGUE_RELU>(a, b, c, s, plan, workspace, stream)
-                : launch_type<BF16, MATMUL_EPILOGUE_NONE>(a, b, c, s, plan, workspace, stream);
-  return relu ? launch_type<F16, MATMUL_EPILOGUE_RELU>(a, b, c, s, plan, workspace, stream)
-              : launch_type<F16, MATMUL_EPILOGUE_NONE>(a, b, c, s, plan, workspace, stream);
+    return relu ? launch_type<BF16, MATMUL_EPILOGUE_RELU>(a, b, c, s, plan, add, workspace, stream)
+                : launch_type<BF16, MATMUL_EPILOGUE_NONE>(a, b, c, s, plan, add, workspace, stream);
+  return relu ? launch_type<F16, MATMUL_EPILOGUE_RELU>(a, b, c, s, plan, add, workspace, stream)
+              : launch_type<F16, MATMUL_EPILOGUE_NONE>(a, b, c, s, plan, add, workspace, stream);
 }
 
 }  // namespace limn

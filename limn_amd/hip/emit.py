@@ -41,7 +41,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from limn_amd.hip import replay, runtime
-from limn_amd.seam import DType, Index, Instr, LoopNest, Op, Opcode, Valid, accumulate_in, bfloat16, float16, float32, float64, int8, int16, int32
+from limn_amd.seam import DType, Index, Instr, LoopNest, Node, Op, Opcode, Valid, accumulate_in, bfloat16, float16, float32, float64, int8, int16, int32
 
 THREADS = 256
 
@@ -1258,18 +1258,82 @@ def is_relu(nest: LoopNest) -> bool:
     )
 
 
-def epilogue_pairs(nests: list[LoopNest], plans: list[Planned], kept: set | None) -> dict[int, int]:
-    """Relu nests to run as their contraction's epilogue: {contraction nest: relu nest}.
+def add_epilogue(nest: LoopNest, total: Node, N: int) -> tuple[int, int | None] | None:
+    """(bias input, residual input or None) when an elementwise nest is exactly out = total + bias
+    or out = res + (total + bias), at the value type of total's dtype (float for bf16 and f16, one
+    rounding at the store), where total (a contraction's output, row-major, its last axis N long)
+    is read at the cell the nest stores, bias along that last axis only (bias[n]), and res at the
+    stored cell: what limn_hip_matmul_add computes in the contraction's store. A bias-add reader of
+    a Linear layer, and one that also adds the residual stream (reference limn/nn.py:27-36 and
+    limn/tensor.py:486-496 build them). Anything else, None."""
+    body = [i for i in nest.instrs if i.opcode not in (Opcode.LOOP, Opcode.ENDLOOP)]
+    extents = {i.dest: i.arg for i in nest.instrs if i.opcode is Opcode.LOOP}
+    loads = [i for i in body if i.opcode is Opcode.LOAD]
+    stores = [i for i in body if i.opcode is Opcode.STORE]
+    arith = [i for i in body if i.opcode is Opcode.ARITH]
+    if len(body) != len(loads) + len(stores) + len(arith) or len(stores) != 1 or len(loads) not in (2, 3):
+        return None
+    if len(arith) != len(loads) - 1 or any(i.arg is not Op.ADD or i.value_type != total.dtype for i in arith):
+        return None
+    ins = nest.kernel.inputs
+    if nest.kernel.target.dtype != total.dtype or any(l.arg[2].bounds for l in loads):
+        return None
+    index = stores[0].arg[1]
+    unit = [v for v, c in index.terms if c == 1]
+    if len(unit) != 1 or extents.get(unit[0]) != N or any(c % N for v, c in index.terms if c != 1):
+        return None
+    n_var = unit[0]
+    slot = {f"in{k}": k for k in range(len(ins))}
+    role: dict[str, tuple[str, int]] = {}  # load dest -> (what it is, input index)
+    for l in loads:
+        k = slot.get(l.arg[0])
+        if k is None or ins[k].dtype != total.dtype:
+            return None
+        if ins[k] is total and l.arg[1] == index:
+            what = "total"
+        elif l.arg[1].terms == ((n_var, 1),) and l.arg[1].const == 0:
+            what = "bias"
+        elif l.arg[1] == index:
+            what = "res"
+        else:
+            return None
+        role[l.dest] = (what, k)
+    kinds = sorted(w for w, _ in role.values())
+    if kinds not in (["bias", "total"], ["bias", "res", "total"]):
+        return None
+    first = arith[0]
+    if sorted(role[x][0] for x in first.srcs if x in role) != ["bias", "total"] or len(set(first.srcs)) != 2:
+        return None
+    last = first
+    if len(arith) == 2:
+        second = arith[1]
+        others = [x for x in second.srcs if x != first.dest]
+        if len(others) != 1 or first.dest not in second.srcs or role.get(others[0], ("", 0))[0] != "res":
+            return None
+        last = second
+    if stores[0].srcs != (last.dest,):
+        return None
+    bias = next(k for w, k in role.values() if w == "bias")
+    res = next((k for w, k in role.values() if w == "res"), None)
+    return bias, res
 
-    The relu crosses a scheduler cut (the SUM is its own kernel), so it may only move into the
-    contraction's store when nothing else needs the SUM's buffer: the relu nest is its only
-    reader among the plan's nests, and it is neither a sink nor read by a CUSTOM call (`kept`,
-    recorded by the device's plan_of; None when unknown, which fuses nothing)."""
+
+def epilogue_pairs(nests: list[LoopNest], plans: list[Planned], kept: set | None) -> tuple[dict[int, int], dict[int, tuple]]:
+    """Readers to run as their contraction's epilogue: ({contraction nest: reader nest}, {reader
+    nest: (bias input, residual input or None)} for the readers that add terms, see add_epilogue;
+    the others are relu nests).
+
+    The reader crosses a scheduler cut (the SUM is its own kernel), so it may only move into the
+    contraction's store when nothing else needs the SUM's buffer: the reader is its only reader
+    among the plan's nests, and it is neither a sink nor read by a CUSTOM call (`kept`, recorded
+    by the device's plan_of; None when unknown, which fuses nothing)."""
     if kept is None:
-        return {}
+        return {}, {}
     pairs: dict[int, int] = {}
+    addends: dict[int, tuple] = {}
     for i, plan in enumerate(plans):
-        if plan.contraction is None:
+        con = plan.contraction
+        if con is None:
             continue
         total = nests[i].kernel.target
         if total in kept:
@@ -1278,10 +1342,16 @@ def epilogue_pairs(nests: list[LoopNest], plans: list[Planned], kept: set | None
         if len(readers) != 1 or readers[0] <= i:
             continue
         j = readers[0]
-        relu = nests[j].kernel.target
-        if is_relu(nests[j]) and relu.dtype == total.dtype and math.prod(relu.shape) == math.prod(total.shape):
+        out = nests[j].kernel.target
+        if is_relu(nests[j]) and out.dtype == total.dtype and math.prod(out.shape) == math.prod(total.shape):
             pairs[i] = j
-    return pairs
+            continue
+        row_major = con.c_n == 1 and con.c_m == con.N and (con.batch == 1 or con.c_batch == con.M * con.N)
+        terms = add_epilogue(nests[j], total, con.N) if row_major else None
+        if terms is not None and math.prod(out.shape) == math.prod(total.shape):
+            pairs[i] = j
+            addends[j] = terms
+    return pairs, addends
 
 
 INLINE_CELLS = 1 << 16  # the largest producer evaluated in its readers instead of launched
@@ -2055,6 +2125,9 @@ class Program:
     # merged column reduces (keyed as `merged`, whose launch is the partials kernel): the fold
     # launch, each member's byte offset in the shared scratch, and the scratch's size
     columns: dict[int, tuple[Launch, list[int], int]] = field(default_factory=dict)
+    # the epilogue readers that add a bias (and a residual): {reader nest: (bias input, residual
+    # input or None)}; the other epilogues are relus
+    addends: dict[int, tuple] = field(default_factory=dict)
 
     def launcher_of(self, key: int) -> int:
         return self.launch_at.get(key, key)
@@ -2091,7 +2164,7 @@ def plan_program(nests: list[LoopNest], kept: set | None, custom_inputs: set | N
     Touches no GPU."""
     streamed = streamed_outputs(nests, kept, custom_inputs)
     plans = [plan_nest(n, stream=k in streamed) for k, n in enumerate(nests)]
-    pairs = epilogue_pairs(nests, plans, kept)
+    pairs, addends = epilogue_pairs(nests, plans, kept)
     fused = {j: i for i, j in pairs.items()}
     for j in fused:
         plans[j] = Planned("", [], notes={"epilogue of": nests[fused[j]].name})
@@ -2130,7 +2203,7 @@ def plan_program(nests: list[LoopNest], kept: set | None, custom_inputs: set | N
     names += [fold.name for fold, _, _ in columns.values()]
     kept_sources = [p.source for k, p in enumerate(plans) if k not in in_run]
     source = PRELUDE + "\n".join(kept_sources + merged_sources) if names else ""
-    return Program(plans, pairs, inlined, merged, source, names, launch_at, columns)
+    return Program(plans, pairs, inlined, merged, source, names, launch_at, columns, addends)
 
 
 def nest_runners(dev, nests: list[LoopNest]):
@@ -2170,7 +2243,7 @@ def nest_runners(dev, nests: list[LoopNest]):
             runners.append(_defer_runner(deferred, k))
         elif role == "epilogue":
             source = next(i for i, j in pairs.items() if j == k)
-            runners.append(_epilogue_runner(dev, plans[source].contraction, operands, source))
+            runners.append(_epilogue_runner(dev, plans[source].contraction, operands, source, prog.addends.get(k)))
         elif role == "contraction":
             runners.append(_contraction_runner(dev, plan.contraction))
         else:
@@ -2250,8 +2323,9 @@ def _keep_runner(producer_inputs: dict, k: int):
     return run
 
 
-def _matmul_launcher(dev, con: Contraction, epilogue: int):
-    """launch(inputs, out_ptr): the contraction through limn_hip_matmul."""
+def _matmul_launcher(dev, con: Contraction, epilogue: int, adds: bool = False):
+    """launch(inputs, out_ptr, bias_ptr, residual_ptr): the contraction through limn_hip_matmul, or
+    through limn_hip_matmul_add when `adds` (the residual read at the output's strides)."""
     from limn_amd.dtypes import ABI_CODE
 
     lib = dev.lib
@@ -2261,12 +2335,18 @@ def _matmul_launcher(dev, con: Contraction, epilogue: int):
     ws_bytes = int(lib.limn_hip_matmul_workspace(code, con.batch, con.M, con.N, con.K))
     held: list = []  # the split-k workspace, allocated on first use and kept with the runner
 
-    def launch(inputs: list, out: int) -> None:
+    def launch(inputs: list, out: int, bias: int | None = None, res: int | None = None) -> None:
         if ws_bytes and not held:
             held.append(dev._alloc(ws_bytes))
         a = inputs[con.a_input].ptr + con.a_offset * size
         b = inputs[con.b_input].ptr + con.b_offset * size
         ws = held[0].ptr if held else None
+        if adds:
+            args = (a, b, out, *shape, bias, 1, res, con.c_batch, con.c_m, con.c_n, ws, ws_bytes)
+            runtime.check_limn(lib.limn_hip_matmul_add(*args, None))
+            if dev.tape is not None:
+                dev.tape.append(replay.Launch(replay.STEP_MATMUL_ADD, args))
+            return
         runtime.check_limn(lib.limn_hip_matmul(a, b, out, *shape, ws, ws_bytes, None))
         if dev.tape is not None:
             dev.tape.append(replay.Launch(replay.STEP_MATMUL, (a, b, out, *shape, ws, ws_bytes)))
@@ -2294,13 +2374,22 @@ def _stash_runner(operands: dict, k: int):
     return run
 
 
-def _epilogue_runner(dev, con: Contraction, operands: dict, k: int):
-    """The relu nest's call: the contraction of nest k with a relu epilogue, stored into this
-    nest's output. Its layout is the contraction's: the relu reads and writes cell for cell."""
-    launch = _matmul_launcher(dev, con, 1)
+def _epilogue_runner(dev, con: Contraction, operands: dict, k: int, terms: tuple | None = None):
+    """The epilogue reader's call: the contraction of nest k, stored into this nest's output with
+    a relu, or (`terms` = (bias input, residual input or None) of this nest) with the bias and
+    residual added. Its layout is the contraction's: the reader reads and writes cell for cell."""
+    if terms is None:
+        launch = _matmul_launcher(dev, con, 1)
+
+        def run(inputs: list, outs: list) -> None:
+            launch(operands.pop(k), outs[0].ptr)
+
+        return run
+    launch = _matmul_launcher(dev, con, 0, adds=True)
+    bias, res = terms
 
     def run(inputs: list, outs: list) -> None:
-        launch(operands.pop(k), outs[0].ptr)
+        launch(operands.pop(k), outs[0].ptr, inputs[bias].ptr, None if res is None else inputs[res].ptr)
 
     return run
 

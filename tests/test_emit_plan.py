@@ -41,7 +41,12 @@ def operands(m: int = 64, k: int = 64, n: int = 48):
 
 def pairs_of(sinks: list[Tensor]) -> dict[int, int]:
     nests, kept = lowered(sinks)
-    return emit.epilogue_pairs(nests, [emit.plan_nest(n) for n in nests], kept)
+    return emit.epilogue_pairs(nests, [emit.plan_nest(n) for n in nests], kept)[0]
+
+
+def addends_of(sinks: list[Tensor]) -> dict[int, tuple]:
+    nests, kept = lowered(sinks)
+    return emit.epilogue_pairs(nests, [emit.plan_nest(n) for n in nests], kept)[1]
 
 
 def test_relu_nest_is_recognised():
@@ -85,13 +90,59 @@ def test_no_fusion_when_a_custom_call_reads_the_sum():
     nests, kept = lowered([out])
     plans = [emit.plan_nest(n) for n in nests]
     assert any(p.contraction is not None for p in plans)
-    assert emit.epilogue_pairs(nests, plans, kept) == {}
+    assert emit.epilogue_pairs(nests, plans, kept) == ({}, {})
 
 
 def test_no_fusion_without_a_record_of_readers():
     a, b = operands()
     nests, _ = lowered([(a @ b).relu()])
-    assert emit.epilogue_pairs(nests, [emit.plan_nest(n) for n in nests], None) == {}
+    assert emit.epilogue_pairs(nests, [emit.plan_nest(n) for n in nests], None) == ({}, {})
+
+
+def bias_operands(m: int = 64, k: int = 64, n: int = 48):
+    a, b = operands(m, k, n)
+    bias = Tensor(rng.standard_normal(n).astype(np.float32), dtype=bfloat16)
+    res = Tensor(rng.standard_normal((m, n)).astype(np.float32), dtype=bfloat16)
+    return a, b, bias, res
+
+
+def test_bias_add_of_a_contraction_becomes_its_epilogue():
+    """A Linear layer's `x @ w + b`: the add reads the sum at the cell it stores and the bias along
+    the last axis, so it runs in the contraction's store (limn_hip_matmul_add)."""
+    a, b, bias, _ = bias_operands()
+    assert pairs_of([a @ b + bias]) == {0: 1}
+    assert addends_of([a @ b + bias]) == {1: (1, None)}
+    assert addends_of([bias + a @ b]) == {1: (0, None)}
+
+
+def test_residual_and_bias_add_becomes_the_epilogue():
+    """The residual stream's `x + (h @ w + b)`: both terms join the store, the bias first."""
+    a, b, bias, res = bias_operands()
+    (terms,) = addends_of([res + (a @ b + bias)]).values()
+    assert terms[1] is not None and terms[0] != terms[1]
+
+
+@pytest.mark.parametrize(
+    "spell",
+    [
+        lambda mm, bias, res: (res + mm) + bias,  # another association: another rounding
+        lambda mm, bias, res: mm + res,  # no bias
+        lambda mm, bias, res: mm * bias,  # not an add
+        lambda mm, bias, res: mm + bias.reshape(1, 48).cast(float32).cast(bfloat16) + bias,  # three terms
+        lambda mm, bias, res: (mm + bias).cast(float32),  # stored at another width
+    ],
+    ids=["residual-first", "residual-only", "scale", "two-biases", "wider"],
+)
+def test_other_adds_are_not_epilogues(spell):
+    a, b, bias, res = bias_operands()
+    assert addends_of([spell(a @ b, bias, res)]) == {}
+
+
+def test_a_bias_along_the_rows_is_not_an_epilogue():
+    """bias[m] (a column vector) is not the n-vector the epilogue adds."""
+    a, b, _, _ = bias_operands()
+    col = Tensor(rng.standard_normal((64, 1)).astype(np.float32), dtype=bfloat16)
+    assert addends_of([a @ b + col]) == {}
 
 
 def test_float32_sum_is_not_a_contraction():
@@ -103,7 +154,7 @@ def test_float32_sum_is_not_a_contraction():
 def inlined_of(sinks: list[Tensor], kept_override=None) -> tuple[list, set[int]]:
     nests, kept = lowered(sinks)
     plans = [emit.plan_nest(n) for n in nests]
-    pairs = emit.epilogue_pairs(nests, plans, kept)
+    pairs = emit.epilogue_pairs(nests, plans, kept)[0]
     return nests, emit.inline_producers(nests, plans, kept if kept_override is None else kept_override(kept), pairs)
 
 
@@ -199,7 +250,7 @@ def runs_of(sinks: list[Tensor]):
     custom = {realized(src) for n in order if n.op is Op.CUSTOM for src in n.srcs}
     kept = {realized(s) for s in nodes} | custom
     plans = [emit.plan_nest(n) for n in nests]
-    pairs = emit.epilogue_pairs(nests, plans, kept)
+    pairs = emit.epilogue_pairs(nests, plans, kept)[0]
     inl = emit.InlineSet(nests, emit.inline_producers(nests, plans, kept, pairs))
     return nests, emit.merge_runs(nests, plans, custom, inl, pairs)[0]
 

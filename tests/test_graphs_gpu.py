@@ -592,6 +592,50 @@ def test_relu_epilogue_matches_the_separate_relu_bit_for_bit(hipdev, m, n, k):
     assert (got >= 0).all()
 
 
+@pytest.mark.parametrize(
+    "m,n,k,residual,dtype",
+    [
+        (200, 72, 1024, False, bfloat16),
+        (200, 72, 1024, True, float16),
+        (256, 128, 4096, True, bfloat16),
+        (96, 40, 200, True, bfloat16),
+        (300, 264, 512, False, bfloat16),
+        (4160, 4096, 64, True, bfloat16),
+    ],
+    ids=["dma", "dma-f16-residual", "split-k", "k-tail", "ragged", "256-tile"],
+)
+def test_bias_epilogue_matches_the_separate_add_bit_for_bit(hipdev, m, n, k, residual, dtype):
+    """`a @ b + bias` and `res + (a @ b + bias)` as one launch of limn_hip_matmul_add (the add
+    nest is the sum's only reader) against the same graph with the sum also a sink, which keeps
+    the add nest separate: the sum rounded once, the terms added in float, one more rounding, so
+    the bits agree. Every store path: the staged 16-byte rows, row tails, the register-staged
+    kernel's element stores (k = 200) and the split-k fold. And against the float64 closed form."""
+    from limn_amd.dtypes import from_storage, to_storage
+    from limn_amd.hip import emit
+    from limn_amd.seam import lower_all, realized, schedule
+
+    def vals(shape):
+        x = rng.standard_normal(shape).astype(np.float32)
+        return from_storage(to_storage(x, dtype).view(np.uint8), dtype, shape).astype(np.float64)
+
+    a_v, b_v, bias_v, res_v = vals((m, k)), vals((k, n)), vals((n,)), vals((m, n))
+    a, b = Tensor(a_v.astype(np.float32), dtype=dtype), Tensor(b_v.astype(np.float32), dtype=dtype)
+    bias, res = Tensor(bias_v.astype(np.float32), dtype=dtype), Tensor(res_v.astype(np.float32), dtype=dtype)
+    mm = a @ b
+    out = res + (mm + bias) if residual else mm + bias
+    nodes = [out.node]
+    order = topological(nodes)
+    nests = lower_all(nodes, order, schedule(nodes, order))
+    _, addends = emit.epilogue_pairs(nests, [emit.plan_nest(x) for x in nests], {realized(x) for x in nodes})
+    assert addends, "the add did not become the contraction's epilogue"
+    fused = hipdev.copyout(hipdev.execute([out.node])[0]).view(np.uint16)
+    _, separate = hipdev.execute([mm.node, out.node])
+    np.testing.assert_array_equal(fused, hipdev.copyout(separate).view(np.uint16))
+    got = from_storage(fused.view(np.uint8), dtype, (m, n)).astype(np.float64)
+    exact = a_v @ b_v + bias_v + (res_v if residual else 0.0)
+    np.testing.assert_allclose(got, exact, rtol=2**-6, atol=2e-2 * np.sqrt(k / 1024) + 2e-2)
+
+
 def test_weight_gradient_is_one_split_k_contraction(hipdev):
     """A weight gradient sums over batch and rows together (K = 8 * 512 = 4096) into a 256 x 128
     output: one contraction, split in k (the output is two 128-tiles), its slices added in order.
