@@ -107,18 +107,19 @@ int limn_hip_matmul(const void* a, const void* b, void* c, int dtype, int64_t ba
 
 /*
  * limn_hip_matmul with terms added at the store: out[b, m, n] = T(residual[b, m, n] +
- * (T(epilogue(sum)) + bias[n])), computed in float with T the rounding to the output type, either
- * term left out when its pointer is null (bias[n] at bias + n * bias_n; residual at r_batch, r_m,
- * r_n element strides). This is an elementwise reader of the contraction that adds a bias vector
+ * (T(epilogue(sum)) + T(bias[n]))), computed in float with T the rounding to the output type, either
+ * term left out when its pointer is null (bias[n] at bias + n * bias_n, of type bias_dtype: the
+ * output's, or LIMN_HIP_FLOAT32 for a float32 bias rounded to the output type first, as a cast
+ * would; the residual of the output type at r_batch, r_m, r_n element strides). This is an elementwise reader of the contraction that adds a bias vector
  * (and a residual), which the device evaluates in the contraction's store instead of a launch of
  * its own: the reference emits such a reader as a separate kernel (limn/cuda_emit.py:287-372,
  * emit_elementwise, after the contraction's emit_tiled). Same workspace rules as limn_hip_matmul.
  */
 int limn_hip_matmul_add(const void* a, const void* b, void* c, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
                         int64_t a_batch, int64_t a_m, int64_t a_k, int64_t b_batch, int64_t b_k, int64_t b_n,
-                        int64_t c_batch, int64_t c_m, int64_t c_n, int epilogue, const void* bias, int64_t bias_n,
-                        const void* residual, int64_t r_batch, int64_t r_m, int64_t r_n, void* workspace,
-                        int64_t workspace_bytes, void* stream);
+                        int64_t c_batch, int64_t c_m, int64_t c_n, int epilogue, const void* bias, int bias_dtype,
+                        int64_t bias_n, const void* residual, int64_t r_batch, int64_t r_m, int64_t r_n,
+                        void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Bytes of workspace limn_hip_matmul uses to split k for this shape; 0 when it does not split. No
  * counterpart in the reference (its contraction kernel never splits). */
@@ -148,7 +149,7 @@ int limn_hip_matmul_supported(int dtype, int64_t M, int64_t N, int64_t K, int64_
  * A pre-bound launch list: the kernels of one recorded execution of a plan, replayed against new
  * buffers. Each step is one launch: a hipRTC module kernel (`function`, `grid` x `block`
  * threads, its arguments the kernel's parameters in order), a zero fill (pointer, bytes), or one
- * call of limn_hip_matmul (its 20 arguments before `stream`), limn_hip_matmul_add (26),
+ * call of limn_hip_matmul (its 20 arguments before `stream`), limn_hip_matmul_add (27),
  * limn_hip_sdpa_fwd (13 before
  * `scale`), limn_hip_sdpa_bwd_q (15) or limn_hip_sdpa_bwd_kv (16), with `scale` in the step. An
  * argument is `value` when `slot` < 0, else slots[slot] + value: a byte offset into the buffer

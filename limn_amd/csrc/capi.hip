@@ -182,16 +182,19 @@ int limn_hip_matmul(const void* a, const void* b, void* c, int dtype, int64_t ba
 
 int limn_hip_matmul_add(const void* a, const void* b, void* c, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
                         int64_t a_batch, int64_t a_m, int64_t a_k, int64_t b_batch, int64_t b_k, int64_t b_n,
-                        int64_t c_batch, int64_t c_m, int64_t c_n, int epilogue, const void* bias, int64_t bias_n,
-                        const void* residual, int64_t r_batch, int64_t r_m, int64_t r_n, void* workspace,
-                        int64_t workspace_bytes, void* stream) {
+                        int64_t c_batch, int64_t c_m, int64_t c_n, int epilogue, const void* bias, int bias_dtype,
+                        int64_t bias_n, const void* residual, int64_t r_batch, int64_t r_m, int64_t r_n,
+                        void* workspace, int64_t workspace_bytes, void* stream) {
   MatmulShape s = {batch, M, N, K, a_batch, a_m, a_k, b_batch, b_k, b_n, c_batch, c_m, c_n};
   const int rc = check_matmul("matmul_add", a, b, c, dtype, s, epilogue);
   if (rc != LIMN_HIP_OK) return rc;
   if (workspace_bytes < 0) return fail(LIMN_HIP_EINVAL, "matmul_add: negative workspace size");
-  if (((uintptr_t)bias | (uintptr_t)residual) % 2 != 0)
-    return fail(LIMN_HIP_EINVAL, "matmul_add: the bias and residual must be 2-byte aligned");
-  MatmulAddends add = {(const u16*)bias, bias_n, (const u16*)residual, r_batch, r_m, r_n, 0};
+  if (bias != nullptr && bias_dtype != dtype && bias_dtype != LIMN_HIP_FLOAT32)
+    return fail(LIMN_HIP_EINVAL, "matmul_add: the bias is of the output type or float32, not dtype %d", bias_dtype);
+  const int f32 = bias != nullptr && bias_dtype == LIMN_HIP_FLOAT32;
+  if ((uintptr_t)bias % (f32 ? 4 : 2) != 0 || (uintptr_t)residual % 2 != 0)
+    return fail(LIMN_HIP_EINVAL, "matmul_add: the bias and residual must be aligned to their element size");
+  MatmulAddends add = {bias, f32, bias_n, (const u16*)residual, r_batch, r_m, r_n, 0};
   if (bias != nullptr && bias_n == 1 && (uintptr_t)bias % 16 == 0) add.vec |= 1;
   if (residual != nullptr && r_n == 1 && r_m % 8 == 0 && r_batch % 8 == 0 && (uintptr_t)residual % 16 == 0) add.vec |= 2;
   return launch_matmul(a, b, c, dtype, s, epilogue, add, workspace, workspace_bytes, (hipStream_t)stream);

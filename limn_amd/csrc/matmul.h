@@ -20,7 +20,8 @@ enum { MATMUL_EPILOGUE_NONE = 0, MATMUL_EPILOGUE_RELU = 1 };
 // left out when its pointer is null. This is an elementwise reader of the contraction that adds a
 // bias vector (and a residual), evaluated at the store instead of in a launch of its own.
 struct MatmulAddends {
-  const u16* bias;  // bias[n * bias_n]
+  const void* bias;  // bias[n * bias_n], of the output type, or float32 rounded to it first
+  int bias_f32;
   int64_t bias_n;
   const u16* res;   // res[b * r_batch + m * r_m + n * r_n]
   int64_t r_batch, r_m, r_n;

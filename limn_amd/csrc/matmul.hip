@@ -54,22 +54,38 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
 // The addends of one output cell: t is the contraction already rounded to T.
 template <typename T>
+__device__ __forceinline__ u16 bias_at(const MatmulAddends& add, int64_t col) {
+  const int64_t i = col * add.bias_n;
+  return add.bias_f32 ? T::pack(((const float*)add.bias)[i]) : ((const u16*)add.bias)[i];
+}
+
+template <typename T>
 __device__ __forceinline__ u16 add_terms(u16 t, const MatmulAddends& add, int64_t bz, int64_t row, int64_t col) {
   float x = T::unpack(t);
-  if (add.bias != nullptr) x = x + T::unpack(add.bias[col * add.bias_n]);
+  if (add.bias != nullptr) x = x + T::unpack(bias_at<T>(add, col));
   if (add.res != nullptr) x = T::unpack(add.res[bz * add.r_batch + row * add.r_m + col * add.r_n]) + x;
   return T::pack(x);
 }
 
-// The bias of 8 consecutive n, and the residual of 8 consecutive n of one row: 16-byte loads where
-// the terms are contiguous and aligned and the 8 cells lie before N (col is a multiple of 8), else
+// The bias of 8 consecutive n (rounded to T when it is float32), and the residual of 8 consecutive
+// n of one row: 16-byte loads where the terms are contiguous and aligned and the 8 cells lie before N (col is a multiple of 8), else
 // element loads; cells past N read zeros (they are not stored).
+template <typename T>
 __device__ __forceinline__ u16x8 bias8(const MatmulAddends& add, int64_t col, int64_t N) {
   u16x8 v = zero8();
   if (add.bias == nullptr) return v;
-  if ((add.vec & 1) && col + 7 < N) return *(const u16x8*)(add.bias + col);
+  if ((add.vec & 1) && col + 7 < N) {
+    if (!add.bias_f32) return *(const u16x8*)((const u16*)add.bias + col);
+    const f32x4 lo = *(const f32x4*)((const float*)add.bias + col), hi = *(const f32x4*)((const float*)add.bias + col + 4);
 #pragma unroll
-  for (int e = 0; e < 8; e++) v[e] = col + e < N ? add.bias[(col + e) * add.bias_n] : (u16)0;
+    for (int e = 0; e < 4; e++) {
+      v[e] = T::pack(lo[e]);
+      v[e + 4] = T::pack(hi[e]);
+    }
+    return v;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) v[e] = col + e < N ? bias_at<T>(add, col + e) : (u16)0;
   return v;
 }
 __device__ __forceinline__ u16x8 res8(const MatmulAddends& add, int64_t bz, int64_t row, int64_t col, int64_t N) {
@@ -504,7 +520,7 @@ __global__ __launch_bounds__(64 * DmaTile<BM>::WAVES, 2) void matmul_dma(const u
     u16x8 bv = zero8(), rv[ITS];
     if (adds) {
       const int64_t col = n0 + wn * WTN + cc * 8;
-      bv = bias8(add, col, s.N);
+      bv = bias8<T>(add, col, s.N);
 #pragma unroll
       for (int it = 0; it < ITS; it++) {
         const int64_t row = m0 + wm * WTM + p * IB * 32 + it * RPI + lane / CPR;

@@ -79,14 +79,14 @@ int run_step(const limn_hip_replay_step& s, int64_t i, const limn_hip_replay_arg
                              (void*)(intptr_t)v[18], v[19], stream);
     }
     case LIMN_HIP_STEP_MATMUL_ADD: {
-      int rc = expect(s, i, 26, "matmul_add");
+      int rc = expect(s, i, 27, "matmul_add");
       if (rc != LIMN_HIP_OK) return rc;
-      int64_t v[26];
-      for (int k = 0; k < 26; k++) v[k] = bound(a[k], slots);
+      int64_t v[27];
+      for (int k = 0; k < 27; k++) v[k] = bound(a[k], slots);
       return limn_hip_matmul_add((const void*)(intptr_t)v[0], (const void*)(intptr_t)v[1], (void*)(intptr_t)v[2], (int)v[3],
                                  v[4], v[5], v[6], v[7], v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15], v[16],
-                                 (int)v[17], (const void*)(intptr_t)v[18], v[19], (const void*)(intptr_t)v[20], v[21],
-                                 v[22], v[23], (void*)(intptr_t)v[24], v[25], stream);
+                                 (int)v[17], (const void*)(intptr_t)v[18], (int)v[19], v[20], (const void*)(intptr_t)v[21],
+                                 v[22], v[23], v[24], (void*)(intptr_t)v[25], v[26], stream);
     }
     case LIMN_HIP_STEP_SDPA_FWD: {
       int rc = expect(s, i, 13, "sdpa");

@@ -1066,6 +1066,51 @@ def fold_parts(name: str, shape: NestShape, acc_t: str, out_dtype: DType, out_re
     return lines, max(1, min(-(-cells // waves), 1 << 20))
 
 
+def fold_columns(name: str, shape: NestShape, acc_t: str, out_dtype: DType, out_ref: str, wide: bool, cells: int,
+                 parts: int, ident: str) -> tuple[list[str], int]:
+    """The fold of a column reduce's partial totals, laid out part-major (`scratch[p_ * cells +
+    g]`): a workgroup takes 64 consecutive cells, lane = cell, so each part it loads is one
+    coalesced 256-byte row; wave w folds the parts w, w + 4, ... in order (16 loads in flight at a
+    time) and wave 0 then folds the 4 waves' totals in wave order. A wave per cell, its lanes
+    loading 64 parts of that cell, read one 4-byte word per 64-byte line: the GPT step's folds of
+    13312 cells x 256 parts took 20 us each at 0.7 TB/s."""
+    fold = shape.fold
+    waves = THREADS // 64
+    tiles = -(-cells // 64)
+    per = -(-parts // waves)
+    lines = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}(const {acc_t}* __restrict__ ALIGNED scratch, {STORE_T[out_dtype]}* __restrict__ ALIGNED out) {{']
+    lines.append("  const int lane = threadIdx.x & 63, w_ = threadIdx.x >> 6;")
+    lines.append(f"  __shared__ {acc_t} fold_[{waves}][64];")
+    lines.append(f"  for (i64 t_ = blockIdx.x; t_ < {tiles}LL; t_ += gridDim.x) {{")
+    lines.append("    const i64 g = t_ * 64 + lane;")
+    lines.append(f"    {acc_t} acc = {ident};")
+    lines.append(f"    if (g < {cells}LL) {{")
+    lines.append(f"      for (int q0_ = 0; q0_ < {per}; q0_ += 16) {{")
+    lines.append(f"        {acc_t} f_[16];")
+    lines.append("#pragma unroll")
+    lines.append(f"        for (int q_ = 0; q_ < 16; q_++) {{")
+    lines.append(f"          const int k_ = w_ + {waves} * (q0_ + q_), p_ = k_ < {parts} ? k_ : {parts - 1};")
+    lines.append(f"          f_[q_] = scratch[p_ * {cells}LL + g];")
+    lines.append("        }")
+    lines.append("#pragma unroll")
+    lines.append(f"        for (int q_ = 0; q_ < 16; q_++)")
+    lines.append(f"          if (w_ + {waves} * (q0_ + q_) < {parts}) " + _fold(fold, "acc", "f_[q_]"))
+    lines.append("      }")
+    lines.append("    }")
+    lines.append("    fold_[w_][lane] = acc;")
+    lines.append("    __syncthreads();")
+    lines.append(f"    if (w_ == 0 && g < {cells}LL) {{")
+    lines.append("      acc = fold_[0][lane];")
+    for w in range(1, waves):
+        lines.append("      " + _fold(fold, "acc", f"fold_[{w}][lane]"))
+    lines += decode(shape.outer, "g", "      ", wide)
+    lines.append(f"      {out_ref} = {store_expr(out_dtype, 'acc')};")
+    lines.append("    }")
+    lines.append("    __syncthreads();")
+    lines += ["  }", "}"]
+    return lines, max(1, min(tiles, 1 << 20))
+
+
 def lane_group(chunks: int) -> int:
     """Lanes per cell of a row reduce over `chunks` vector chunks, under 256 of them (see
     plan_reduce's short rows)."""
@@ -1190,7 +1235,10 @@ def plan_columns(nest: LoopNest, shape: NestShape, bufs: Buffers, cells: int, R:
     launches = [Launch(name, tiles * parts, THREADS, "io" if parts == 1 else "io_scratch")]
     if parts == 1:
         return Planned("\n".join(lines), launches, notes={"columns": True, "parts": 1, "vec": vec})
-    final, final_grid = fold_parts(nest.name, shape, acc_t, out_dtype, out_ref, wide, cells, parts, ident, f"p_ * {cells}LL + g")
+    if parts > 16:
+        final, final_grid = fold_columns(nest.name, shape, acc_t, out_dtype, out_ref, wide, cells, parts, ident)
+    else:
+        final, final_grid = fold_parts(nest.name, shape, acc_t, out_dtype, out_ref, wide, cells, parts, ident, f"p_ * {cells}LL + g")
     launches.append(Launch(nest.name, final_grid, THREADS, "scratch_out"))
     return Planned("\n".join(lines) + "\n" + "\n".join(final), launches, scratch_bytes=cells * parts * acc_dt.itemsize,
                    notes={"columns": True, "parts": parts, "vec": vec})
@@ -1320,8 +1368,8 @@ def add_epilogue(nest: LoopNest, total: Node, N: int) -> tuple[int, int | None] 
 
 def epilogue_pairs(nests: list[LoopNest], plans: list[Planned], kept: set | None) -> tuple[dict[int, int], dict[int, tuple]]:
     """Readers to run as their contraction's epilogue: ({contraction nest: reader nest}, {reader
-    nest: (bias input, residual input or None)} for the readers that add terms, see add_epilogue;
-    the others are relu nests).
+    nest: (bias input, residual input or None, the bias's cast nest or None)} for the readers that
+    add terms, see add_epilogue and bias_cast; the others are relu nests).
 
     The reader crosses a scheduler cut (the SUM is its own kernel), so it may only move into the
     contraction's store when nothing else needs the SUM's buffer: the reader is its only reader
@@ -1350,8 +1398,36 @@ def epilogue_pairs(nests: list[LoopNest], plans: list[Planned], kept: set | None
         terms = add_epilogue(nests[j], total, con.N) if row_major else None
         if terms is not None and math.prod(out.shape) == math.prod(total.shape):
             pairs[i] = j
-            addends[j] = terms
+            addends[j] = (*terms, bias_cast(nests, nests[j].kernel.inputs[terms[0]], j, kept))
     return pairs, addends
+
+
+def bias_cast(nests: list[LoopNest], bias: Node, reader: int, kept: set) -> int | None:
+    """The nest that makes an add epilogue's bias, when the epilogue can take over its work: a
+    nest that only rounds a float32 vector to the bias's type (a bf16 Linear bias cast from its
+    float32 parameter), read by nothing but the fused reader. limn_hip_matmul_add then reads the
+    float32 vector and rounds it itself (the cast's own arithmetic), and the cast launches
+    nothing; launched alone, each such cast cost a 4-5 us launch in the GPT step."""
+    if bias in kept:
+        return None
+    makers = [p for p, n in enumerate(nests) if n.kernel.target is bias]
+    if len(makers) != 1 or makers[0] >= reader:
+        return None
+    p = makers[0]
+    if any(bias in n.kernel.inputs for k, n in enumerate(nests) if k != reader):
+        return None
+    nest = nests[p]
+    body = [i for i in nest.instrs if i.opcode not in (Opcode.LOOP, Opcode.ENDLOOP)]
+    loops = [i for i in nest.instrs if i.opcode is Opcode.LOOP]
+    if len(body) != 3 or len(loops) != 1 or len(nest.kernel.inputs) != 1 or nest.kernel.inputs[0].dtype != float32:
+        return None
+    load, cast, store = body
+    index = Index(0, ((loops[0].dest, 1),))
+    if (load.opcode is not Opcode.LOAD or load.arg[0] != "in0" or load.arg[1] != index or load.arg[2].bounds
+            or cast.opcode is not Opcode.CAST or cast.srcs != (load.dest,) or cast.value_type != bias.dtype
+            or store.opcode is not Opcode.STORE or store.srcs != (cast.dest,) or store.arg[1] != index):
+        return None
+    return p
 
 
 INLINE_CELLS = 1 << 16  # the largest producer evaluated in its readers instead of launched
@@ -2126,7 +2202,8 @@ class Program:
     # launch, each member's byte offset in the shared scratch, and the scratch's size
     columns: dict[int, tuple[Launch, list[int], int]] = field(default_factory=dict)
     # the epilogue readers that add a bias (and a residual): {reader nest: (bias input, residual
-    # input or None)}; the other epilogues are relus
+    # input or None, the nest whose float32 input the epilogue rounds into the bias, or None)};
+    # the other epilogues are relus
     addends: dict[int, tuple] = field(default_factory=dict)
 
     def launcher_of(self, key: int) -> int:
@@ -2168,7 +2245,8 @@ def plan_program(nests: list[LoopNest], kept: set | None, custom_inputs: set | N
     fused = {j: i for i, j in pairs.items()}
     for j in fused:
         plans[j] = Planned("", [], notes={"epilogue of": nests[fused[j]].name})
-    inlined = InlineSet(nests, inline_producers(nests, plans, kept, pairs))
+    absorbed = {terms[2] for terms in addends.values() if terms[2] is not None}
+    inlined = InlineSet(nests, inline_producers(nests, plans, kept, pairs) | absorbed)
     for c, nest in enumerate(nests):
         if c not in inlined.producers and plans[c].launches and inlined.reached(nest):
             plans[c] = plan_nest(nest, inlined, stream=c in streamed)
@@ -2243,7 +2321,8 @@ def nest_runners(dev, nests: list[LoopNest]):
             runners.append(_defer_runner(deferred, k))
         elif role == "epilogue":
             source = next(i for i, j in pairs.items() if j == k)
-            runners.append(_epilogue_runner(dev, plans[source].contraction, operands, source, prog.addends.get(k)))
+            runners.append(_epilogue_runner(dev, plans[source].contraction, operands, source, prog.addends.get(k),
+                                            producer_inputs))
         elif role == "contraction":
             runners.append(_contraction_runner(dev, plan.contraction))
         else:
@@ -2335,14 +2414,14 @@ def _matmul_launcher(dev, con: Contraction, epilogue: int, adds: bool = False):
     ws_bytes = int(lib.limn_hip_matmul_workspace(code, con.batch, con.M, con.N, con.K))
     held: list = []  # the split-k workspace, allocated on first use and kept with the runner
 
-    def launch(inputs: list, out: int, bias: int | None = None, res: int | None = None) -> None:
+    def launch(inputs: list, out: int, bias: int | None = None, res: int | None = None, bias_code: int = code) -> None:
         if ws_bytes and not held:
             held.append(dev._alloc(ws_bytes))
         a = inputs[con.a_input].ptr + con.a_offset * size
         b = inputs[con.b_input].ptr + con.b_offset * size
         ws = held[0].ptr if held else None
         if adds:
-            args = (a, b, out, *shape, bias, 1, res, con.c_batch, con.c_m, con.c_n, ws, ws_bytes)
+            args = (a, b, out, *shape, bias, bias_code, 1, res, con.c_batch, con.c_m, con.c_n, ws, ws_bytes)
             runtime.check_limn(lib.limn_hip_matmul_add(*args, None))
             if dev.tape is not None:
                 dev.tape.append(replay.Launch(replay.STEP_MATMUL_ADD, args))
@@ -2374,10 +2453,13 @@ def _stash_runner(operands: dict, k: int):
     return run
 
 
-def _epilogue_runner(dev, con: Contraction, operands: dict, k: int, terms: tuple | None = None):
+def _epilogue_runner(dev, con: Contraction, operands: dict, k: int, terms: tuple | None = None,
+                     producer_inputs: dict | None = None):
     """The epilogue reader's call: the contraction of nest k, stored into this nest's output with
-    a relu, or (`terms` = (bias input, residual input or None) of this nest) with the bias and
-    residual added. Its layout is the contraction's: the reader reads and writes cell for cell."""
+    a relu, or (`terms` = (bias input, residual input or None, bias cast nest or None) of this
+    nest) with the bias and residual added; a bias whose cast nest the epilogue took over is that
+    nest's float32 input. Its layout is the contraction's: the reader reads and writes cell for
+    cell."""
     if terms is None:
         launch = _matmul_launcher(dev, con, 1)
 
@@ -2386,10 +2468,14 @@ def _epilogue_runner(dev, con: Contraction, operands: dict, k: int, terms: tuple
 
         return run
     launch = _matmul_launcher(dev, con, 0, adds=True)
-    bias, res = terms
+    bias, res, cast = terms
+    from limn_amd.dtypes import ABI_CODE
+
+    bias_code = ABI_CODE[float32 if cast is not None else con.dtype]
 
     def run(inputs: list, outs: list) -> None:
-        launch(operands.pop(k), outs[0].ptr, inputs[bias].ptr, None if res is None else inputs[res].ptr)
+        bias_ptr = producer_inputs[cast][0].ptr if cast is not None else inputs[bias].ptr
+        launch(operands.pop(k), outs[0].ptr, bias_ptr, None if res is None else inputs[res].ptr, bias_code)
 
     return run
 

@@ -32,7 +32,7 @@ STEP_KERNEL, STEP_ZERO, STEP_MATMUL, STEP_SDPA_FWD, STEP_SDPA_BWD_Q, STEP_SDPA_B
 POINTER_ARGS = {
     STEP_ZERO: frozenset({0}),
     STEP_MATMUL: frozenset({0, 1, 2, 18}),
-    STEP_MATMUL_ADD: frozenset({0, 1, 2, 18, 20, 24}),
+    STEP_MATMUL_ADD: frozenset({0, 1, 2, 18, 21, 25}),
     STEP_SDPA_FWD: frozenset(range(6)),
     STEP_SDPA_BWD_Q: frozenset(range(8)),
     STEP_SDPA_BWD_KV: frozenset(range(9)),

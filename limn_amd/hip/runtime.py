@@ -82,7 +82,7 @@ _LIMN = {
     "limn_hip_matmul": (c_int, [c_void_p, c_void_p, c_void_p, c_int] + [_I64] * 13 + [c_int, c_void_p, _I64, c_void_p]),
     "limn_hip_matmul_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_int] + [_I64] * 13 + [c_int, c_void_p]),
     "limn_hip_matmul_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int] + [_I64] * 13
-                            + [c_int, c_void_p, _I64, c_void_p, _I64, _I64, _I64, c_void_p, _I64, c_void_p]),
+                            + [c_int, c_void_p, c_int, _I64, c_void_p, _I64, _I64, _I64, c_void_p, _I64, c_void_p]),
     "limn_hip_matmul_workspace": (_I64, [c_int, _I64, _I64, _I64, _I64]),
     "limn_hip_replay": (c_int, [c_void_p, _I64, c_void_p, _I64, c_void_p, _I64, c_void_p]),
     "limn_hip_replay_graph": (c_int, [c_void_p, _I64, c_void_p, _I64, c_void_p, _I64, c_void_p]),

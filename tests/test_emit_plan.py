@@ -111,8 +111,27 @@ def test_bias_add_of_a_contraction_becomes_its_epilogue():
     the last axis, so it runs in the contraction's store (limn_hip_matmul_add)."""
     a, b, bias, _ = bias_operands()
     assert pairs_of([a @ b + bias]) == {0: 1}
-    assert addends_of([a @ b + bias]) == {1: (1, None)}
-    assert addends_of([bias + a @ b]) == {1: (0, None)}
+    assert addends_of([a @ b + bias]) == {1: (1, None, None)}
+    assert addends_of([bias + a @ b]) == {1: (0, None, None)}
+
+
+def test_a_cast_bias_is_rounded_by_the_epilogue():
+    """A bf16 bias cast from a float32 parameter (as the GPT's Linear layers make it): the cast
+    nest, read only by the fused add, is absorbed (the epilogue rounds the float32 vector
+    itself) and launches nothing; a cast something else also reads stays a nest."""
+    a, b = operands()
+    w = Tensor(rng.standard_normal(48).astype(np.float32), dtype=float32)
+    nests, kept = lowered([a @ b + w.cast(bfloat16)])
+    plans = [emit.plan_nest(n) for n in nests]
+    pairs, addends = emit.epilogue_pairs(nests, plans, kept)
+    ((j, (bias, res, cast)),) = addends.items()
+    assert cast is not None and nests[cast].kernel.target is nests[j].kernel.inputs[bias]
+    prog = emit.plan_program(nests, kept, set())
+    assert prog.role(cast) == "inlined" and not prog.plans[cast].launches
+    wb = w.cast(bfloat16)
+    nests, kept = lowered([a @ b + wb, wb * 2.0])
+    _, addends = emit.epilogue_pairs(nests, [emit.plan_nest(n) for n in nests], kept)
+    assert [t[2] for t in addends.values()] == [None]
 
 
 def test_residual_and_bias_add_becomes_the_epilogue():

@@ -601,15 +601,20 @@ def test_relu_epilogue_matches_the_separate_relu_bit_for_bit(hipdev, m, n, k):
         (96, 40, 200, True, bfloat16),
         (300, 264, 512, False, bfloat16),
         (4160, 4096, 64, True, bfloat16),
+        (200, 72, 1024, "cast", bfloat16),
+        (256, 128, 4096, "cast", float16),
+        (96, 40, 200, "cast", bfloat16),
     ],
-    ids=["dma", "dma-f16-residual", "split-k", "k-tail", "ragged", "256-tile"],
+    ids=["dma", "dma-f16-residual", "split-k", "k-tail", "ragged", "256-tile", "cast-bias", "cast-bias-split-k-f16",
+         "cast-bias-k-tail"],
 )
 def test_bias_epilogue_matches_the_separate_add_bit_for_bit(hipdev, m, n, k, residual, dtype):
     """`a @ b + bias` and `res + (a @ b + bias)` as one launch of limn_hip_matmul_add (the add
     nest is the sum's only reader) against the same graph with the sum also a sink, which keeps
     the add nest separate: the sum rounded once, the terms added in float, one more rounding, so
     the bits agree. Every store path: the staged 16-byte rows, row tails, the register-staged
-    kernel's element stores (k = 200) and the split-k fold. And against the float64 closed form."""
+    kernel's element stores (k = 200) and the split-k fold; "cast": the bias a float32 vector cast
+    to the operand type, which the epilogue rounds itself. And against the float64 closed form."""
     from limn_amd.dtypes import from_storage, to_storage
     from limn_amd.hip import emit
     from limn_amd.seam import lower_all, realized, schedule
@@ -621,6 +626,11 @@ def test_bias_epilogue_matches_the_separate_add_bit_for_bit(hipdev, m, n, k, res
     a_v, b_v, bias_v, res_v = vals((m, k)), vals((k, n)), vals((n,)), vals((m, n))
     a, b = Tensor(a_v.astype(np.float32), dtype=dtype), Tensor(b_v.astype(np.float32), dtype=dtype)
     bias, res = Tensor(bias_v.astype(np.float32), dtype=dtype), Tensor(res_v.astype(np.float32), dtype=dtype)
+    if residual == "cast":
+        bias_f32 = rng.standard_normal(n).astype(np.float32)
+        bias_v = from_storage(to_storage(bias_f32, dtype).view(np.uint8), dtype, (n,)).astype(np.float64)
+        bias = Tensor(bias_f32, dtype=float32).cast(dtype)
+        residual = False
     mm = a @ b
     out = res + (mm + bias) if residual else mm + bias
     nodes = [out.node]
