@@ -98,18 +98,26 @@ __device__ __forceinline__ u16x8 res8(const MatmulAddends& add, int64_t bz, int6
   return v;
 }
 
-// 8 rounded contraction cells (packed two to a word) with their terms added, rounded again.
+// 8 rounded contraction cells (packed two to a word) with their terms added, rounded again: the
+// two cells of a word unpacked from it and rounded back into one word together (pack2)
 template <typename T>
 __device__ __forceinline__ u32x4 add_terms8(u32x4 w, u16x8 bv, u16x8 rv, const MatmulAddends& add) {
-  u16x8 t = __builtin_bit_cast(u16x8, w);
+  const u32x4 b = __builtin_bit_cast(u32x4, bv), r = __builtin_bit_cast(u32x4, rv);
+  u32x4 out;
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    float x = T::unpack(t[e]);
-    if (add.bias != nullptr) x = x + T::unpack(bv[e]);
-    if (add.res != nullptr) x = T::unpack(rv[e]) + x;
-    t[e] = T::pack(x);
+  for (int e = 0; e < 4; e++) {
+    float lo = T::unpack((u16)(w[e] & 0xFFFFu)), hi = T::unpack((u16)(w[e] >> 16));
+    if (add.bias != nullptr) {
+      lo = lo + T::unpack((u16)(b[e] & 0xFFFFu));
+      hi = hi + T::unpack((u16)(b[e] >> 16));
+    }
+    if (add.res != nullptr) {
+      lo = T::unpack((u16)(r[e] & 0xFFFFu)) + lo;
+      hi = T::unpack((u16)(r[e] >> 16)) + hi;
+    }
+    out[e] = T::pack2(lo, hi);
   }
-  return __builtin_bit_cast(u32x4, t);
+  return out;
 }
 
 // One operand's LDS tile per stage, kept in its memory orientation:

@@ -1066,12 +1066,16 @@ def fold_parts(name: str, shape: NestShape, acc_t: str, out_dtype: DType, out_re
     return lines, max(1, min(-(-cells // waves), 1 << 20))
 
 
+FOLD_LOADS = 64  # partials a lane of a column fold loads at once
+
+
 def fold_columns(name: str, shape: NestShape, acc_t: str, out_dtype: DType, out_ref: str, wide: bool, cells: int,
                  parts: int, ident: str) -> tuple[list[str], int]:
     """The fold of a column reduce's partial totals, laid out part-major (`scratch[p_ * cells +
     g]`): a workgroup takes 64 consecutive cells, lane = cell, so each part it loads is one
-    coalesced 256-byte row; wave w folds the parts w, w + 4, ... in order (16 loads in flight at a
-    time) and wave 0 then folds the 4 waves' totals in wave order. A wave per cell, its lanes
+    coalesced 256-byte row; wave w folds the parts w, w + 4, ... in order (up to FOLD_LOADS of
+    them loaded at once: with a few hundred workgroups each wave's loads must all be in flight
+    together) and wave 0 then folds the 4 waves' totals in wave order. A wave per cell, its lanes
     loading 64 parts of that cell, read one 4-byte word per 64-byte line: the GPT step's folds of
     13312 cells x 256 parts took 20 us each at 0.7 TB/s."""
     fold = shape.fold
@@ -1085,15 +1089,16 @@ def fold_columns(name: str, shape: NestShape, acc_t: str, out_dtype: DType, out_
     lines.append("    const i64 g = t_ * 64 + lane;")
     lines.append(f"    {acc_t} acc = {ident};")
     lines.append(f"    if (g < {cells}LL) {{")
-    lines.append(f"      for (int q0_ = 0; q0_ < {per}; q0_ += 16) {{")
-    lines.append(f"        {acc_t} f_[16];")
+    chunk = min(per, FOLD_LOADS)
+    lines.append(f"      for (int q0_ = 0; q0_ < {per}; q0_ += {chunk}) {{")
+    lines.append(f"        {acc_t} f_[{chunk}];")
     lines.append("#pragma unroll")
-    lines.append(f"        for (int q_ = 0; q_ < 16; q_++) {{")
+    lines.append(f"        for (int q_ = 0; q_ < {chunk}; q_++) {{")
     lines.append(f"          const int k_ = w_ + {waves} * (q0_ + q_), p_ = k_ < {parts} ? k_ : {parts - 1};")
     lines.append(f"          f_[q_] = scratch[p_ * {cells}LL + g];")
     lines.append("        }")
     lines.append("#pragma unroll")
-    lines.append(f"        for (int q_ = 0; q_ < 16; q_++)")
+    lines.append(f"        for (int q_ = 0; q_ < {chunk}; q_++)")
     lines.append(f"          if (w_ + {waves} * (q0_ + q_) < {parts}) " + _fold(fold, "acc", "f_[q_]"))
     lines.append("      }")
     lines.append("    }")
