@@ -2071,6 +2071,7 @@ def row_source(name: str, nests: list[LoopNest], plans: list[Planned], run: list
             out.append(f"{indent}  if (c_ >= {chunks}LL) break;")
         return out, True
 
+    first_param: dict = {}  # (input node, element type) -> the first parameter that carries it
     for s_, (c, m) in enumerate(members):
         nest, plan, shape = nests[c], plans[c], m.shape
         kernel = nest.kernel
@@ -2087,7 +2088,12 @@ def row_source(name: str, nests: list[LoopNest], plans: list[Planned], run: list
         for ctype, pname, const in plan.notes["params"]:
             q = "const " if const else ""
             params.append(f"{q}{ctype}* __restrict__ ALIGNED s{s_}_{pname}")
-            binds.append(f"      {q}{ctype}* __restrict__ {pname} = ({q}{ctype}*)__builtin_assume_aligned(s{s_}_{pname}, 16);")
+            # an input an earlier member (or name) also reads is read through that member's
+            # parameter, so the compiler sees one pointer and shares the loads and the
+            # arithmetic on them (a LayerNorm backward's members all scale dy by gamma)
+            node = names.get(pname) if const else None
+            source = first_param.setdefault((node, ctype), f"s{s_}_{pname}") if node is not None else f"s{s_}_{pname}"
+            binds.append(f"      {q}{ctype}* __restrict__ {pname} = ({q}{ctype}*)__builtin_assume_aligned({source}, 16);")
         var = f"rv{s_}_"
         if m.kind != "cells":
             lines.append(f"    float {var};")
