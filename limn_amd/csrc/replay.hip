@@ -17,7 +17,7 @@ using namespace limn;
 
 namespace {
 
-constexpr int MAX_ARGS = 256;  // a merged launch of up to 16 nests takes at most a few dozen pointers
+constexpr int MAX_ARGS = 512;  // a merged launch takes at most 400 pointers (the emitter's MERGE_PARAMS)
 
 // A zero fill as a kernel rather than hipMemsetAsync, so the list can be captured into a graph
 // (memset nodes of captured graphs have given wrong results on replays after the first): 16-byte

@@ -1564,8 +1564,8 @@ def inline_producers(nests: list[LoopNest], plans: list[Planned], kept: set | No
 
 MERGE_GRID = 1 << 16  # the largest elementwise launch merged with its neighbours
 MERGE_GROUP_GRID = 1 << 20  # the most workgroups of one merged launch
-MERGE_MEMBERS = 16  # the most nests in one merged launch
-MERGE_PARAMS = 160  # the most pointers one merged launch takes
+MERGE_MEMBERS = 48  # the most nests in one merged launch
+MERGE_PARAMS = 400  # the most pointers one merged launch takes (3.2 KB of its 4 KB of arguments)
 
 
 def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set | None, inlined: "InlineSet",
