@@ -403,6 +403,36 @@ def test_a_read_of_another_row_ends_the_row_program():
     assert any(len(run) == 2 for run in runs)  # max and sum still share a row program
 
 
+def test_row_program_members_read_a_shared_input_through_one_pointer():
+    """Members of a row program that read the same buffer (a LayerNorm backward's members all
+    read dy and gamma) bind it from the first member's parameter, so the compiler sees one
+    pointer and shares the loads and the arithmetic on them; every member keeps its own
+    parameter in the signature, so the launch's arguments do not change."""
+    from limn_amd.seam import grad, nn
+    x = Tensor(rng.standard_normal((64, 512)).astype(np.float32), dtype=bfloat16, requires_grad=True)
+    ln = nn.LayerNorm(512)
+    (gx,) = grad((ln(x).cast(float32) * Tensor(rng.standard_normal((64, 512)).astype(np.float32))).sum(), [x])
+    nests, kept = lowered([gx])
+    prog = emit.plan_program(nests, kept, set())
+    rows = [(run, launch) for run, launch in prog.merged.values() if "_rows_" in launch.name]
+    assert rows
+    shared = 0
+    for run, launch in rows:
+        src = prog.source[prog.source.index(f"void {launch.name}("):]
+        end = src.find('extern "C"')
+        src = src if end < 0 else src[:end]
+        signature = src[: src.index(") {")]
+        first: dict = {}
+        for c_s, c in enumerate(run):
+            for k, node in enumerate(nests[c].kernel.inputs):
+                assert f"s{c_s}_in{k}" in signature  # the parameter stays
+                if node in first and first[node][0] != c_s:
+                    shared += 1
+                    assert f"__builtin_assume_aligned(s{c_s}_in{k}, 16)" not in src, (launch.name, c_s, k)
+                first.setdefault(node, (c_s, k))
+    assert shared > 0, "no member of the program shares an input"
+
+
 def test_a_row_program_never_caches_an_inlined_producer():
     """A small producer evaluated where it is read (a materialized x * 2 + a broadcast row, as the
     GPT's embedding sum) feeding a LayerNorm: its output buffer is never written, so the row
