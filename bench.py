@@ -745,7 +745,7 @@ def main() -> int:
         return 0
     from limn_amd.dtypes import bf16_bits, bf16_values
     from limn_amd.hip.device import HipDevice
-    from limn_amd.hip.runtime import hip_unavailable
+    from limn_amd.hip.runtime import check_limn, hip_unavailable
     from limn_amd.seam import Node, Op, Tensor, bfloat16, custom, float32, topological
 
     reason = hip_unavailable()
@@ -781,18 +781,35 @@ def main() -> int:
     delta = Node(Op.BUFFER, (), float32, (B, H, S, 1), delta_buf)
     lse_node = Node(Op.BUFFER, (), float32, (B, H, S, 1), lse)
     srcs = (q, k, v, do, lse_node, delta)
+    # limn's backward: two CUSTOM calls on the same inputs (reference limn/tensor.py:707-712),
+    # which the device's plan runs as one call (the dK/dV pass hands dS to the dQ pass)
     (dq_node,) = custom("sdpa_bwd_q", srcs, (True, scale), ((bfloat16, (B, H, S, D)),))
-    dk_node, _ = custom("sdpa_bwd_kv", srcs, (True, scale), ((bfloat16, (B, H, S, D)), (bfloat16, (B, H, S, D))))
-    bwd_q, bwd_kv = dev.custom_runner(dq_node), dev.custom_runner(dk_node)
+    dk_node, dv_node = custom("sdpa_bwd_kv", srcs, (True, scale), ((bfloat16, (B, H, S, D)), (bfloat16, (B, H, S, D))))
+    bwd_sinks = [dq_node, dk_node, dv_node]
+    order = topological(bwd_sinks)
+    bwd_plan = dev.plan_of(order, {n: i for i, n in enumerate(order)}, bwd_sinks)
+    assert len(bwd_plan.calls) == 1 and len(bwd_plan.calls[0].outputs) == 3, "the backward pair runs as one call"
+    bwd_call = bwd_plan.calls[0].fn
     dq, dk, dv = (dev.out_alloc(B * H * S * D * 2, False) for _ in range(3))
     ins_fwd = [q.arg, k.arg, v.arg]
     ins_bwd = [q.arg, k.arg, v.arg, do.arg, lse, delta.arg]
+    bwd_call(ins_bwd, [dq, dk, dv])  # allocates the call's own hand-off workspace
+    dev.finish()
+    # the call's two kernels, timed one at a time through the C ABI's `passes` (same kernels, same
+    # order, on a workspace of the same size)
+    code = 3  # LIMN_HIP_BFLOAT16
+    ws_bytes = int(dev.lib.limn_hip_sdpa_bwd_workspace(code, B * H, S, S, D, D, 1, 0))
+    ws = dev.out_alloc(ws_bytes, False)
+    bwd_args = (*[b.ptr for b in ins_bwd], None, dq.ptr, dk.ptr, dv.ptr, code, B * H, S, S, D, D, 1, scale)
+
+    def bwd_pass(passes: int) -> None:
+        check_limn(dev.lib.limn_hip_sdpa_bwd(*bwd_args, passes, ws.ptr, ws_bytes, None))
 
     stages = (
         lambda: fwd(ins_fwd, [out, lse]),
         lambda: delta_fn(delta_ins, [delta_buf]),
-        lambda: bwd_q(ins_bwd, [dq]),
-        lambda: bwd_kv(ins_bwd, [dk, dv]),
+        lambda: bwd_pass(1),
+        lambda: bwd_pass(2),
     )
     for _ in range(args.warmup):
         for stage in stages:
@@ -817,17 +834,27 @@ def main() -> int:
     per /= args.steps
     ms = total_ms / args.steps
 
+    # the paired backward call as a whole, timed the way the device runs it
+    ev_call = Events(dev.api, 2)
+    ev_call.record(0)
+    for _ in range(args.steps):
+        bwd_call(ins_bwd, [dq, dk, dv])
+    ev_call.record(1)
+    dev.finish()
+    bwd_call_ms = ev_call.ms(0, 1) / args.steps
+
     U = 2.0 * B * H * S * S * D / 2
     step_flops = 7 * U
-    kernel_flops = {"sdpa": 2 * U, "delta": 0.0, "sdpa_bwd_q": 1 * U, "sdpa_bwd_kv": 4 * U}
-    names = ["sdpa", "delta", "sdpa_bwd_q", "sdpa_bwd_kv"]
+    # the dK/dV pass computes S, dP, dV and dK (4U); the dQ pass dQ from the handed-over dS (1U)
+    kernel_flops = {"sdpa": 2 * U, "delta": 0.0, "sdpa_bwd_kv": 4 * U, "sdpa_bwd_q": 1 * U}
+    names = ["sdpa", "delta", "sdpa_bwd_kv", "sdpa_bwd_q"]
     delta_bytes = 2 * B * H * S * D * 2 + B * H * S * 4  # dO and O read, delta written
     custom_ms = float(per[0] + per[2] + per[3])
     # the template instance each CUSTOM name runs at this configuration (rocprofv3's kernel names)
     KERNEL_SYMBOL = {
         "sdpa": "sdpa_fwd_dma<BF16,true,false>",
-        "sdpa_bwd_q": "sdpa_bwd_q_dma<BF16,true,false>",
-        "sdpa_bwd_kv": "sdpa_bwd_kv_piped<BF16,true>",
+        "sdpa_bwd_kv": "sdpa_bwd_kv_piped<BF16,true,true>",
+        "sdpa_bwd_q": "sdpa_dq_ds<BF16,true>",
     }
     dom = int(np.argmax(per))
     achieved = kernel_flops[names[dom]] / (per[dom] * 1e-3)
@@ -846,7 +873,7 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "C4 causal flash attention fwd+bwd (sdpa, sdpa_bwd_q, sdpa_bwd_kv)",
+            "workload": "C4 causal flash attention fwd+bwd (sdpa, then sdpa_bwd_q + sdpa_bwd_kv as one paired call)",
             "batch": B,
             "heads": H,
             "seq_len": S,
@@ -856,6 +883,13 @@ def main() -> int:
         },
         "mfma_peak_frac": round(value / MFMA_BF16_PEAK, 4),
         "kernels_ms": {n: round(float(t), 4) for n, t in zip(names, per)},
+        "backward_call": {
+            "note": "sdpa_bwd_q and sdpa_bwd_kv as the device's plan runs them: one call, the dK/dV pass "
+                    "(S, dP, dV, dK, and dS stored) then the dQ pass reading dS (2 bytes per visited pair)",
+            "ms": round(bwd_call_ms, 4),
+            "handoff_bytes": ws_bytes,
+            "dq_pass_GB_s": round((ws_bytes + B * H * S * D * 2 * 2) / (per[3] * 1e-3) / 1e9, 1),
+        },
         "custom_kernels": {
             "note": "the three CUSTOM kernels alone, the north star's 40% target (the step adds the delta nest)",
             "ms": round(custom_ms, 4),
@@ -884,6 +918,7 @@ def main() -> int:
         inputs = [bf16_values(h.reshape(B, H, S, D)[:1, :1]) for h in host]
         line["cpu_numpy_oracle"] = cpu_baseline(*inputs, scale, B, H, step_flops)
     del q, k, v, do, out, lse, dq, dk, dv, delta, lse_node, o_node, l_node, dq_node, dk_node, delta_buf, delta_ins, o_t
+    del dv_node, bwd_sinks, order, bwd_plan, bwd_call, ws
     cpu = not args.no_cpu
     if args.headline_only:
         print(json.dumps(line), flush=True)

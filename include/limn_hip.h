@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define LIMN_HIP_ABI_VERSION 2
+#define LIMN_HIP_ABI_VERSION 3
 
 enum {
   LIMN_HIP_FLOAT64 = 0,
@@ -90,6 +90,31 @@ int limn_hip_sdpa_bwd_kv(const void* q, const void* k, const void* v, const void
                          int64_t hd, int64_t hd_v, int causal, double scale, void* stream);
 
 /*
+ * Both backward kernels of fused attention in one call: dq as limn_hip_sdpa_bwd_q defines it, dk
+ * and dv as limn_hip_sdpa_bwd_kv does. limn's backward issues them as two CUSTOM calls on the same
+ * inputs (reference limn/tensor.py:707-712: "sdpa_bwd_q", "sdpa_bwd_kv"; kernels
+ * limn/cuda_emit.py:968-1083); the device runs such a pair as this one call. Given a workspace
+ * of limn_hip_sdpa_bwd_workspace(...) bytes, the dK/dV pass hands the dS it computes (2 bytes per
+ * (query, key) pair it visits) to the dQ pass through the workspace, and the dQ pass reads it
+ * instead of recomputing S, dP and the softmax; without one (null, smaller, or a call with no such
+ * route) the two passes run as the separate entry points run them. dq may differ between the two
+ * routes in rounding; each route is deterministic. `passes` is LIMN_HIP_BWD_BOTH for callers;
+ * LIMN_HIP_BWD_KV_PASS and LIMN_HIP_BWD_Q_PASS run one pass each (the dQ pass reads the dS the
+ * dK/dV pass of an earlier call on the same workspace left there), so a harness can time each.
+ */
+enum { LIMN_HIP_BWD_KV_PASS = 1, LIMN_HIP_BWD_Q_PASS = 2, LIMN_HIP_BWD_BOTH = 3 };
+int limn_hip_sdpa_bwd(const void* q, const void* k, const void* v, const void* dout, const void* lse, const void* delta,
+                      const void* key_mask, void* dq, void* dk, void* dv, int dtype, int64_t batch, int64_t t_q, int64_t t_k,
+                      int64_t hd, int64_t hd_v, int causal, double scale, int passes, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes limn_hip_sdpa_bwd hands dS through for such a call (masked: a key mask is
+ * given); 0 when the call has no such route (today: bf16/f16 at hd == hd_v == 128 without a key
+ * mask, and keys in whole 128-row blocks unless causal). No counterpart in the reference. */
+int64_t limn_hip_sdpa_bwd_workspace(int dtype, int64_t batch, int64_t t_q, int64_t t_k, int64_t hd, int64_t hd_v, int causal,
+                                    int masked);
+
+/*
  * Dense contraction on matrix cores: c[b, m, n] = epilogue(sum_k a[b, m, k] * b[b, k, n]), bf16 or
  * f16 operands and result, f32 accumulation. Strides are in elements; each operand must be
  * contiguous along k or along its row (m / n) with the other stride a multiple of 8.
@@ -151,7 +176,8 @@ int limn_hip_matmul_supported(int dtype, int64_t M, int64_t N, int64_t K, int64_
  * threads, its arguments the kernel's parameters in order), a zero fill (pointer, bytes), or one
  * call of limn_hip_matmul (its 20 arguments before `stream`), limn_hip_matmul_add (27),
  * limn_hip_sdpa_fwd (13 before
- * `scale`), limn_hip_sdpa_bwd_q (15) or limn_hip_sdpa_bwd_kv (16), with `scale` in the step. An
+ * `scale`), limn_hip_sdpa_bwd_q (15), limn_hip_sdpa_bwd_kv (16) or limn_hip_sdpa_bwd (17 before
+ * `scale`, then passes, workspace and its size: 20), with `scale` in the step. An
  * argument is `value` when `slot` < 0, else slots[slot] + value: a byte offset into the buffer
  * this replay binds to that slot. Steps run in order on `stream`; the first failing one stops the
  * list and its status is returned. No counterpart in the reference: its capture replays a plan
@@ -165,6 +191,7 @@ enum {
   LIMN_HIP_STEP_SDPA_BWD_Q = 4,
   LIMN_HIP_STEP_SDPA_BWD_KV = 5,
   LIMN_HIP_STEP_MATMUL_ADD = 6,
+  LIMN_HIP_STEP_SDPA_BWD = 7,
 };
 
 typedef struct {

@@ -33,11 +33,32 @@ def hipcc() -> str:
     return path
 
 
+def _includes(path: Path, seen: set[Path]) -> set[Path]:
+    """The quoted #include files `path` reaches (transitively), resolved next to it or in include/."""
+    for line in path.read_text().splitlines():
+        line = line.strip()
+        if not line.startswith('#include "'):
+            continue
+        name = line.split('"')[1]
+        for base in (path.parent, INCLUDE):
+            dep = (base / name).resolve()
+            if dep.exists():
+                if dep not in seen:
+                    seen.add(dep)
+                    _includes(dep, seen)
+                break
+    return seen
+
+
 def _stale(obj: Path, src: Path, headers: list[Path]) -> bool:
+    """Whether obj is older than its source or a header the source includes (`headers` bounds the
+    search to the project's own headers)."""
     if not obj.exists():
         return True
     t = obj.stat().st_mtime
-    return any(p.stat().st_mtime > t for p in [src, *headers])
+    own = set(headers)
+    deps = [h for h in _includes(src, set()) if h in own]
+    return any(p.stat().st_mtime > t for p in [src, *deps])
 
 
 def _compile(src: Path, obj: Path) -> None:

@@ -170,6 +170,37 @@ int limn_hip_sdpa_bwd_kv(const void* q, const void* k, const void* v, const void
   return run(SDPA_BWD_KV, a);
 }
 
+int64_t limn_hip_sdpa_bwd_workspace(int dtype, int64_t batch, int64_t t_q, int64_t t_k, int64_t hd, int64_t hd_v, int causal,
+                                    int masked) {
+  static const char one = 0;  // a stand-in key mask: only its presence matters here
+  SdpaArgs a = {nullptr, nullptr, nullptr, nullptr,     nullptr, nullptr, masked ? &one : nullptr, nullptr, nullptr, dtype,
+                batch,   t_q,     t_k,     hd,          hd_v,    causal != 0, 1.0, nullptr};
+  if (batch < 1 || t_q < 1 || t_k < 1 || (causal && t_q != t_k)) return 0;
+  return mfma_bwd_workspace(a);
+}
+
+int limn_hip_sdpa_bwd(const void* q, const void* k, const void* v, const void* dout, const void* lse, const void* delta,
+                      const void* key_mask, void* dq, void* dk, void* dv, int dtype, int64_t batch, int64_t t_q, int64_t t_k,
+                      int64_t hd, int64_t hd_v, int causal, double scale, int passes, void* workspace,
+                      int64_t workspace_bytes, void* stream) {
+  SdpaArgs a = {q,     k,   v,   dout, lse,  delta,       key_mask, dq,   dk, dtype,
+                batch, t_q, t_k, hd,   hd_v, causal != 0, scale,    (hipStream_t)stream};
+  a.out2 = dv;
+  int rc = validate(SDPA_BWD_Q, a);
+  if (rc != LIMN_HIP_OK) return rc;
+  if (dk == nullptr || dv == nullptr) return fail(LIMN_HIP_EINVAL, "sdpa_bwd: null dk/dv buffer");
+  if (workspace_bytes < 0) return fail(LIMN_HIP_EINVAL, "sdpa_bwd: negative workspace size");
+  if (passes < LIMN_HIP_BWD_KV_PASS || passes > LIMN_HIP_BWD_BOTH) return fail(LIMN_HIP_EINVAL, "sdpa_bwd: passes must be 1, 2 or 3");
+  const int64_t need = mfma_bwd_workspace(a);
+  if (need > 0 && workspace != nullptr && workspace_bytes >= need) return launch_mfma_bwd(a, workspace, passes);
+  // no hand-off: the two passes as their own entry points run them
+  SdpaArgs kv = a;
+  kv.out0 = dk;
+  kv.out1 = dv;
+  rc = passes & LIMN_HIP_BWD_Q_PASS ? run(SDPA_BWD_Q, a) : LIMN_HIP_OK;
+  return rc != LIMN_HIP_OK || !(passes & LIMN_HIP_BWD_KV_PASS) ? rc : run(SDPA_BWD_KV, kv);
+}
+
 int limn_hip_matmul(const void* a, const void* b, void* c, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
                     int64_t a_batch, int64_t a_m, int64_t a_k, int64_t b_batch, int64_t b_k, int64_t b_n, int64_t c_batch,
                     int64_t c_m, int64_t c_n, int epilogue, void* workspace, int64_t workspace_bytes, void* stream) {

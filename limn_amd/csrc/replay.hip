@@ -117,6 +117,17 @@ int run_step(const limn_hip_replay_step& s, int64_t i, const limn_hip_replay_arg
                                   (const void*)(intptr_t)v[6], (void*)(intptr_t)v[7], (void*)(intptr_t)v[8], (int)v[9], v[10],
                                   v[11], v[12], v[13], v[14], (int)v[15], s.scale, stream);
     }
+    case LIMN_HIP_STEP_SDPA_BWD: {
+      int rc = expect(s, i, 20, "sdpa_bwd");
+      if (rc != LIMN_HIP_OK) return rc;
+      int64_t v[20];
+      for (int k = 0; k < 20; k++) v[k] = bound(a[k], slots);
+      return limn_hip_sdpa_bwd((const void*)(intptr_t)v[0], (const void*)(intptr_t)v[1], (const void*)(intptr_t)v[2],
+                               (const void*)(intptr_t)v[3], (const void*)(intptr_t)v[4], (const void*)(intptr_t)v[5],
+                               (const void*)(intptr_t)v[6], (void*)(intptr_t)v[7], (void*)(intptr_t)v[8], (void*)(intptr_t)v[9],
+                               (int)v[10], v[11], v[12], v[13], v[14], v[15], (int)v[16], s.scale, (int)v[17], (void*)(intptr_t)v[18],
+                               v[19], stream);
+    }
     default:
       return fail(LIMN_HIP_EINVAL, "replay step %lld: unknown kind %d", (long long)i, s.kind);
   }

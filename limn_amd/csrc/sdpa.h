@@ -21,6 +21,7 @@ struct SdpaArgs {
   bool causal;
   double scale;
   hipStream_t stream;
+  void* out2 = nullptr;  // dv of the fused backward (out0 = dq, out1 = dk there)
 };
 
 enum SdpaPass { SDPA_FWD = 0, SDPA_BWD_Q = 1, SDPA_BWD_KV = 2 };
@@ -29,6 +30,15 @@ enum SdpaPass { SDPA_FWD = 0, SDPA_BWD_Q = 1, SDPA_BWD_KV = 2 };
 bool mfma_supports(int dtype, int64_t hd, int64_t hd_v);
 bool mfma_fits(int64_t t_q, int64_t t_k, int64_t hd);
 int launch_sdpa_mfma(SdpaPass pass, const SdpaArgs& a);
+// one pass each, in its own translation unit (sdpa_mfma_fwd/bwd_q/bwd_kv.hip)
+int launch_mfma_fwd(const SdpaArgs& a);
+int launch_mfma_bwd_q(const SdpaArgs& a);
+int launch_mfma_bwd_kv(const SdpaArgs& a);
+// Both backward passes through the dS hand-off (sdpa_mfma_bwd.hip): the workspace bytes it needs
+// for this call, 0 when the call has no such route (only D = 128 without a key mask, keys in whole
+// 128-row blocks unless causal); and the launch, out0 = dq, out1 = dk, out2 = dv.
+int64_t mfma_bwd_workspace(const SdpaArgs& a);
+int launch_mfma_bwd(const SdpaArgs& a, void* ws, int passes);  // LIMN_HIP_BWD_* bits
 
 // General-width kernels: any float dtype, max(hd, hd_v) <= 256.
 bool rows_supports(int dtype, int64_t hd, int64_t hd_v);

@@ -266,6 +266,12 @@ __global__ __launch_bounds__(THREADS) void sdpa_bwd_q_rows(
   }
 #pragma unroll
   for (int e = 0; e < P; e++) g[e] = group_sum<SPLIT>(g[e]);
+  // a row whose every key is hidden has L = -inf: each of its probabilities is
+  // exp(-inf - (-inf)) = NaN in the numpy reference (reference limn/sdpa.py:140-170), so its dQ is NaN
+  if (L == -__builtin_inf()) {
+#pragma unroll
+    for (int e = 0; e < P; e++) g[e] = __builtin_nan("");
+  }
   if (valid && grp == 0) store_row<T, MAXD>(dq + b * t_q * hd, g, i, hd, u, C(1));
 }
 
@@ -299,9 +305,12 @@ __global__ __launch_bounds__(THREADS) void sdpa_bwd_kv_rows(
     gv[e] = C(0);
   }
   // a causal key j is seen by queries i >= j only, so the block starts at its own first key;
-  // every thread meets the same barriers.
+  // every thread meets the same barriers. A hidden key streams its queries too, with each
+  // probability exp(-inf - L): zero, so its dK and dV stay exactly zero, except against a row
+  // whose every key is hidden (L = -inf), where the numpy reference's probability is NaN
+  // (reference limn/sdpa.py:173-203) and so are the key's gradients.
   const int64_t first = causal ? chunk * ROWS : 0;
-  const int64_t rows_end = live ? t_q : 0;
+  const int64_t rows_end = valid ? t_q : 0;
   for (int64_t r0 = first; r0 < t_q; r0 += STREAM) {
     stage<T, MAXD>(Qt, q + b * t_q * hd, r0, t_q, hd);
     stage<T, MAXD>(Ot, dout + b * t_q * hd_v, r0, t_q, hd_v);
@@ -320,7 +329,7 @@ __global__ __launch_bounds__(THREADS) void sdpa_bwd_kv_rows(
       const int li = (int)(i - r0);
       const C s = dot<T, MAXD>(kv, Qt[li], u);
       const C dp = dot<T, MAXD>(vv, Ot[li], u);
-      const C p = exp_c<C>(s * scale - Lt[li]);
+      const C p = exp_c<C>((live ? s * scale : -__builtin_inf()) - Lt[li]);
       const C ds = p * (dp - Dt[li]) * scale;
 #pragma unroll
       for (int e = 0; e < P; e++) {

@@ -17,6 +17,7 @@ this GPU rather than translated:
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 import math
 import time
 from typing import Any
@@ -31,6 +32,7 @@ from limn_amd.seam import FLOATS, CompiledDevice, LoopNest, Node, Op, Runner, ac
 Buffer = Any
 
 SDPA, SDPA_BWD_Q, SDPA_BWD_KV = "sdpa", "sdpa_bwd_q", "sdpa_bwd_kv"
+BWD_BOTH = 3  # LIMN_HIP_BWD_BOTH: limn_hip_sdpa_bwd runs both passes
 
 
 # One workgroup per table entry (value, target, bytes <= 64 KiB, 16-byte aligned starts): 16-byte
@@ -355,10 +357,41 @@ class HipDevice(CompiledDevice):
         a contraction's epilogue may absorb a relu nest only when no one else reads the sum."""
         self.plan_kept, self.plan_custom_inputs = plan_context(order, sinks)
         try:
-            return super().plan_of(order, position, sinks)
+            plan = super().plan_of(order, position, sinks)
         finally:
             self.plan_kept = None
             self.plan_custom_inputs = None
+        return self._pair_backward(plan)
+
+    # the most workspace one backward pair may hold for its dS hand-off
+    SDPA_HANDOFF_CAP = 8 << 30
+
+    def _pair_backward(self, plan):
+        """Run each sdpa_bwd_q call and the sdpa_bwd_kv call on the same inputs and params as one
+        call (limn_hip_sdpa_bwd), at the first one's place: both read only those inputs, so every
+        one is ready there. Through one call the dK/dV pass hands its dS to the dQ pass instead of
+        the dQ pass recomputing it. Pairs whose call has no hand-off route stay as they are."""
+        calls = list(plan.calls)
+        tags = [getattr(c.fn, "sdpa_pair", None) for c in calls]
+        drop: set[int] = set()
+        for i, tag in enumerate(tags):
+            if tag is None or tag[0] != SDPA_BWD_Q or i in drop:
+                continue
+            j = next((j for j, other in enumerate(tags) if other is not None and other[0] == SDPA_BWD_KV
+                      and other[1] == tag[1] and calls[j].inputs == calls[i].inputs and j not in drop), None)
+            if j is None:
+                continue
+            fused = tag[2]()
+            if fused is None:
+                continue
+            q_call, kv_call = calls[i], calls[j]
+            first = min(i, j)
+            calls[first] = dataclasses.replace(q_call, fn=fused, outputs=q_call.outputs + kv_call.outputs,
+                                               out_nbytes=q_call.out_nbytes + kv_call.out_nbytes)
+            drop.add(max(i, j))
+        if not drop:
+            return plan
+        return dataclasses.replace(plan, calls=tuple(c for k, c in enumerate(calls) if k not in drop))
 
     def runners(self, nests: list[LoopNest]) -> list[Runner]:
         from limn_amd.hip.emit import nest_runners
@@ -437,4 +470,30 @@ class HipDevice(CompiledDevice):
 
         else:
             raise NotImplementedError(f"HipDevice has no kernel for custom op {name!r}")
+        if name != SDPA:
+            # plan_of pairs the two backward calls of one attention through this tag (_pair_backward)
+            run.sdpa_pair = (name, (code, *ints, scale_f, masked), lambda: self._fused_backward(code, ints, scale_f, masked))
+        return run
+
+    def _fused_backward(self, code: int, ints: tuple, scale: float, masked: bool) -> Runner | None:
+        """The runner of a paired backward call (outputs dq, dk, dv) through limn_hip_sdpa_bwd, or
+        None when the call has no dS hand-off route or its workspace would pass SDPA_HANDOFF_CAP.
+        The workspace is allocated on the first run and kept with the runner, so a replayed or
+        graph-captured list sees the same pointer every time."""
+        lib = self.lib
+        need = int(lib.limn_hip_sdpa_bwd_workspace(code, *ints, int(masked)))
+        if need <= 0 or need > self.SDPA_HANDOFF_CAP:
+            return None
+        held: list = []
+
+        def run(inputs: list[Buffer], outs: list[Buffer]) -> None:
+            if not held:
+                held.append(self._alloc(need))
+            ws = held[0]
+            mask = inputs[6].ptr if masked else None
+            args = (*[b.ptr for b in inputs[:6]], mask, outs[0].ptr, outs[1].ptr, outs[2].ptr, code, *ints)
+            check_limn(lib.limn_hip_sdpa_bwd(*args, scale, BWD_BOTH, ws.ptr, ws.nbytes, None))
+            if self.tape is not None:
+                self.tape.append(replay.Launch(replay.STEP_SDPA_BWD, (*args, BWD_BOTH, ws.ptr, ws.nbytes), scale=scale))
+
         return run

@@ -26,7 +26,8 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-STEP_KERNEL, STEP_ZERO, STEP_MATMUL, STEP_SDPA_FWD, STEP_SDPA_BWD_Q, STEP_SDPA_BWD_KV, STEP_MATMUL_ADD = range(7)
+(STEP_KERNEL, STEP_ZERO, STEP_MATMUL, STEP_SDPA_FWD, STEP_SDPA_BWD_Q, STEP_SDPA_BWD_KV, STEP_MATMUL_ADD,
+ STEP_SDPA_BWD) = range(8)
 
 # which arguments of each step kind are device pointers (the rest are sizes, codes and flags)
 POINTER_ARGS = {
@@ -36,6 +37,7 @@ POINTER_ARGS = {
     STEP_SDPA_FWD: frozenset(range(6)),
     STEP_SDPA_BWD_Q: frozenset(range(8)),
     STEP_SDPA_BWD_KV: frozenset(range(9)),
+    STEP_SDPA_BWD: frozenset(range(10)) | {18},
 }
 
 ARG = np.dtype([("value", np.int64), ("slot", np.int32), ("reserved", np.int32)])

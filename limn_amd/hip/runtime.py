@@ -27,7 +27,7 @@ P = ctypes.POINTER
 c_int64 = ctypes.c_int64
 
 ARCH = "gfx950"
-ABI_VERSION = 2  # LIMN_HIP_ABI_VERSION of include/limn_hip.h
+ABI_VERSION = 3  # LIMN_HIP_ABI_VERSION of include/limn_hip.h
 LIBRARY = Path(__file__).resolve().parent.parent / "liblimn_hip.so"
 
 # hipMemcpyKind
@@ -103,6 +103,11 @@ _LIMN = {
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, _I64, _I64,
          _I64, _I64, _I64, c_int, ctypes.c_double, c_void_p],
     ),
+    "limn_hip_sdpa_bwd": (
+        c_int,
+        [c_void_p] * 10 + [c_int, _I64, _I64, _I64, _I64, _I64, c_int, ctypes.c_double, c_int, c_void_p, _I64, c_void_p],
+    ),
+    "limn_hip_sdpa_bwd_workspace": (_I64, [c_int, _I64, _I64, _I64, _I64, _I64, c_int, c_int]),
 }
 
 # The C ABI's status codes (include/limn_hip.h) and the Python exception each maps to.

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert runtime.kernels().limn_hip_abi_version() == runtime.ABI_VERSION == 2
+    assert runtime.kernels().limn_hip_abi_version() == runtime.ABI_VERSION == 3
 
 
 def test_sdpa_path_routing():

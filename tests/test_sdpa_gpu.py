@@ -40,7 +40,8 @@ def forward(dev, q, k, v, mask, causal, dtype_name):
     return download(dev, bo, dtype, o.shape), download(dev, bl, accumulate_in(dtype), lse.shape)
 
 
-def backward(dev, q, k, v, do, lse, delta, mask, causal, dtype_name):
+def backward_nodes(dev, q, k, v, do, lse, delta, mask, causal, dtype_name):
+    """The (dq, dk, dv) nodes of limn's backward: two CUSTOM calls on the same inputs."""
     dtype = DTYPES[dtype_name]
     stat = accumulate_in(dtype)
     scale = q.shape[-1] ** -0.5
@@ -49,8 +50,23 @@ def backward(dev, q, k, v, do, lse, delta, mask, causal, dtype_name):
         srcs.append(upload(dev, mask, dtype))
     (dq,) = custom("sdpa_bwd_q", tuple(srcs), (causal, scale), ((dtype, q.shape),))
     dk, dv = custom("sdpa_bwd_kv", tuple(srcs), (causal, scale), ((dtype, k.shape), (dtype, v.shape)))
-    bufs = dev.execute([dq, dk, dv])
-    return [download(dev, b, dtype, n.shape) for b, n in zip(bufs, (dq, dk, dv))]
+    return dq, dk, dv
+
+
+def backward(dev, q, k, v, do, lse, delta, mask, causal, dtype_name):
+    """Both backward calls in one execution, as limn's gradients() realizes them: the device may
+    run the pair as one call (dS handed from the dK/dV pass to the dQ pass)."""
+    nodes = backward_nodes(dev, q, k, v, do, lse, delta, mask, causal, dtype_name)
+    bufs = dev.execute(list(nodes))
+    return [download(dev, b, DTYPES[dtype_name], n.shape) for b, n in zip(bufs, nodes)]
+
+
+def backward_separately(dev, q, k, v, do, lse, delta, mask, causal, dtype_name):
+    """The two backward calls in two executions, so nothing pairs them: each pass on its own."""
+    dq, dk, dv = backward_nodes(dev, q, k, v, do, lse, delta, mask, causal, dtype_name)
+    (bq,) = dev.execute([dq])
+    bk, bv = dev.execute([dk, dv])
+    return [download(dev, b, DTYPES[dtype_name], n.shape) for b, n in zip((bq, bk, bv), (dq, dk, dv))]
 
 
 def draw(seed, q_shape, k_shape, v_shape, dtype_name, live=None):
@@ -256,3 +272,86 @@ def test_config4_full_size_every_xcd(hipdev):
         want_dk, want_dv = ref.sdpa_backward_kv(*bargs, causal=True, scale=scale, dtype="bfloat16", block_size=256)
         for name, got, want in (("dQ", dq[b, h], want_dq), ("dK", dk[b, h], want_dk), ("dV", dv[b, h], want_dv)):
             np.testing.assert_allclose(got, want, rtol=3e-2, atol=3e-2, err_msg=f"{name} head {flat}")
+
+
+# The dS hand-off route (limn_hip_sdpa_bwd): D = 128 without a key mask, causal or with whole
+# 128-key blocks; ragged query tiles, several key blocks, rectangular non-causal.
+HANDOFF_CASES = {
+    "causal_ragged": (((2, 1, 333, 128), (2, 1, 333, 128), (2, 1, 333, 128)), True),
+    "causal_long": (((1, 2, 640, 128), (1, 2, 640, 128), (1, 2, 640, 128)), True),
+    "full_square": (((1, 2, 384, 128), (1, 2, 384, 128), (1, 2, 384, 128)), False),
+    "full_ragged_queries": (((2, 200, 128), (2, 256, 128), (2, 256, 128)), False),
+}
+
+
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float16"])
+@pytest.mark.parametrize("case", sorted(HANDOFF_CASES))
+def test_paired_backward_hands_ds_to_the_dq_pass(hipdev, case, dtype_name):
+    """An sdpa_bwd_q / sdpa_bwd_kv pair on the same inputs is one call of the plan, whose dK/dV
+    pass hands dS to the dQ pass. It matches the oracle; against the two passes run on their
+    own, dK and dV come from the same dK/dV pass (the same bits) and dQ from the other route
+    (within the bf16 tolerance); and it gives the same bits twice."""
+    from limn_amd.seam import topological
+
+    shapes, causal = HANDOFF_CASES[case]
+    q, k, v, do, _ = draw(9, *shapes, dtype_name)
+    scale = q.shape[-1] ** -0.5
+    out, lse = forward(hipdev, q, k, v, None, causal, dtype_name)
+    delta = (do.astype(np.float64) * out).sum(axis=-1, keepdims=True).astype(lse.dtype)
+    nodes = backward_nodes(hipdev, q, k, v, do, lse, delta, None, causal, dtype_name)
+    order = topological(list(nodes))
+    plan = hipdev.plan_of(order, {n: i for i, n in enumerate(order)}, list(nodes))
+    assert len(plan.calls) == 1 and len(plan.calls[0].outputs) == 3, "the pair runs as one call"
+    paired = backward(hipdev, q, k, v, do, lse, delta, None, causal, dtype_name)
+    args = (q, k, v, do, lse, delta, None)
+    want = [ref.sdpa_backward_q(*args, causal=causal, scale=scale, dtype=dtype_name),
+            *ref.sdpa_backward_kv(*args, causal=causal, scale=scale, dtype=dtype_name)]
+    tol = BWD_TOL[dtype_name]
+    for name, got, w in zip(("dq", "dk", "dv"), paired, want):
+        np.testing.assert_allclose(got, w, rtol=tol, atol=tol, err_msg=name)
+    alone = backward_separately(hipdev, q, k, v, do, lse, delta, None, causal, dtype_name)
+    np.testing.assert_array_equal(paired[1], alone[1], err_msg="dk")
+    np.testing.assert_array_equal(paired[2], alone[2], err_msg="dv")
+    np.testing.assert_allclose(paired[0], alone[0], rtol=tol, atol=tol, err_msg="dq")
+    again = backward(hipdev, q, k, v, do, lse, delta, None, causal, dtype_name)
+    for a, b in zip(paired, again):
+        np.testing.assert_array_equal(a, b)
+
+
+HIDDEN_FAMILIES = {"rows_f32": ("float32", 16), "mfma_d64_bf16": ("bfloat16", 64), "mfma_d128_bf16": ("bfloat16", 128)}
+
+
+@pytest.mark.parametrize("family", sorted(HIDDEN_FAMILIES))
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_a_batch_row_with_every_key_hidden(hipdev, family, causal):
+    """A query row with no visible key gives NaN and L = -inf (reference limn/sdpa.py:110-112,
+    126-129). Batch row 0 hides every key, batch row 1 a run of keys. The backward is NaN exactly
+    where the numpy reference's is (every probability of a row with L = -inf is
+    exp(-inf - (-inf))): all of batch row 0's dQ, dK and dV; batch row 1 matches the reference,
+    its hidden keys with exactly zero dK and dV."""
+    dtype_name, hd = HIDDEN_FAMILIES[family]
+    shape = (2, 150, hd)
+    q, k, v, do, _ = draw(10, shape, shape, shape, dtype_name)
+    mask = np.ones((2, 150), np.float64 if dtype_name == "float64" else np.float32)
+    mask[0] = 0
+    mask[1, 40:90] = 0
+    scale = hd**-0.5
+    out, lse = forward(hipdev, q, k, v, mask, causal, dtype_name)
+    want_out, want_lse = ref.sdpa(q, k, v, mask, causal=causal, scale=scale, dtype=dtype_name)
+    assert np.isnan(want_out[0]).all() and np.isneginf(want_lse[0]).all()
+    assert np.isnan(out[0]).all() and np.isneginf(lse[0]).all()
+    tol = FWD_TOL[dtype_name]
+    np.testing.assert_allclose(out[1], want_out[1], rtol=tol, atol=tol)
+    np.testing.assert_allclose(lse[1], want_lse[1], rtol=tol, atol=tol)
+    with np.errstate(invalid="ignore"):
+        delta = (do.astype(np.float64) * out).sum(axis=-1, keepdims=True).astype(lse.dtype)
+    got = backward(hipdev, q, k, v, do, lse, delta, mask, causal, dtype_name)
+    args = (q, k, v, do, lse, delta, mask)
+    want = [ref.sdpa_backward_q(*args, causal=causal, scale=scale, dtype=dtype_name),
+            *ref.sdpa_backward_kv(*args, causal=causal, scale=scale, dtype=dtype_name)]
+    tol = BWD_TOL[dtype_name]
+    for name, g, w in zip(("dq", "dk", "dv"), got, want):
+        assert np.isnan(w[0]).all() and not np.isnan(w[1]).any(), name
+        np.testing.assert_array_equal(np.isnan(g), np.isnan(w), err_msg=f"{name}: NaN positions")
+        np.testing.assert_allclose(g[1], w[1], rtol=tol, atol=tol, err_msg=name)
+    assert (got[1][1, 40:90] == 0).all() and (got[2][1, 40:90] == 0).all()
