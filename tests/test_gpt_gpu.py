@@ -10,7 +10,7 @@ import math
 import numpy as np
 import pytest
 
-from limn_amd.seam import bfloat16, capture, grad, nn, set_seed
+from limn_amd.seam import CompiledDevice, bfloat16, capture, grad, nn, set_seed
 from limn_amd.seam import device as limn_device
 from limn_amd.gpt import GPT, GPTConfig, cross_entropy, make_trainer, synthetic_batch
 from oracle import sdpa as ref
@@ -46,8 +46,15 @@ def test_small_gpt_step_matches_the_oracle(hipdev):
 
 
 def test_small_gpt_training_captured_equals_uncaptured(hipdev):
+    """Captured training (the hip device replays its launch lists through HIP graphs) against
+    the same steps on a device that runs every plan call by call and never records."""
+    from limn_amd.hip.device import HipDevice
+
+    plain = HipDevice()
+    plain.run = lambda plan, sources: CompiledDevice.run(plain, plan, sources)
+
     def run(captured: bool):
-        limn_device.active_device = hipdev
+        limn_device.active_device = hipdev if captured else plain
         set_seed(4)
         model, opt, step = make_trainer(SMALL, lr=1e-3)
         fn = capture(step) if captured else step

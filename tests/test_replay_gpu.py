@@ -3,14 +3,15 @@ records every launch, later runs replay the list in one native call (limn_amd/hi
 Each case runs one graph structure four times with new inputs and checks every result bit for bit
 against a device made to run call by call, covering emitted nests with inlined producers, an
 ordered scatter (a zero-filled output), a contraction with its relu epilogue, and attention
-forward and backward (CUSTOM calls, merged launches)."""
+forward and backward (CUSTOM calls, merged launches), a bf16 Linear with its bias and a residual
+added in the contraction's store, and a contraction whose k is split."""
 
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
-from limn_amd.seam import CompiledDevice, Tensor, bfloat16, grad, nn, realize, scatter_rows
+from limn_amd.seam import CompiledDevice, Tensor, bfloat16, grad, nn, realize, scatter_rows, set_seed
 from limn_amd.seam import device as limn_device
 
 pytestmark = pytest.mark.gpu
@@ -34,6 +35,32 @@ def matmul_relu(seed):
     return [(a @ b).relu()]
 
 
+def linear_bias_residual(seed):
+    """A bf16 Linear with its float32 bias cast at use, added to a residual stream, as the GPT's
+    blocks spell it: one contraction with the bias and the residual added at its store."""
+    from limn_amd.gpt import mixed
+
+    set_seed(seed)
+    layer = nn.Linear(256, 384)
+    r = np.random.default_rng(seed)
+    x = Tensor(r.standard_normal((4, 128, 256)).astype(np.float32), dtype=bfloat16)
+    res = Tensor(r.standard_normal((4, 128, 384)).astype(np.float32), dtype=bfloat16)
+    return [res + mixed(layer, x)]
+
+
+SPLIT_K = (256, 256, 8192)  # (M, N, K): 4 output tiles and a long k, so k splits
+
+
+def split_k(seed):
+    """Few output tiles and a long k: slices of k in float32 partials (a fixed workspace the
+    runner holds) folded in slice order by a second kernel."""
+    m, n, k = SPLIT_K
+    r = np.random.default_rng(seed)
+    a = Tensor(r.standard_normal((m, k)).astype(np.float32), dtype=bfloat16)
+    b = Tensor(r.standard_normal((k, n)).astype(np.float32), dtype=bfloat16)
+    return [a @ b]
+
+
 def attention(seed):
     r = np.random.default_rng(seed)
     q, k, v = (Tensor(r.standard_normal((2, 2, 200, 64)).astype(np.float32), dtype=bfloat16, requires_grad=True) for _ in range(3))
@@ -42,7 +69,14 @@ def attention(seed):
     return [out, *grad((out.float() * w).sum(), [q, k, v])]
 
 
-CASES = {"softmax_layernorm": softmax_layernorm, "scatter": scatter, "matmul_relu": matmul_relu, "attention": attention}
+CASES = {"softmax_layernorm": softmax_layernorm, "scatter": scatter, "matmul_relu": matmul_relu, "attention": attention,
+         "linear_bias_residual": linear_bias_residual, "split_k": split_k}
+
+
+def test_the_split_k_case_splits(hipdev):
+    from limn_amd.dtypes import ABI_CODE
+
+    assert hipdev.lib.limn_hip_matmul_workspace(ABI_CODE[bfloat16], 1, *SPLIT_K) > 0
 
 
 def results(dev, build, seed) -> list[np.ndarray]:
