@@ -16,6 +16,7 @@ this GPU rather than translated:
 
 from __future__ import annotations
 
+import collections
 import ctypes
 import dataclasses
 import math
@@ -131,9 +132,10 @@ class HipDevice(CompiledDevice):
         self.custom[SDPA] = self._sdpa_runner
         self.custom[SDPA_BWD_Q] = self._sdpa_runner
         self.custom[SDPA_BWD_KV] = self._sdpa_runner
-        # pre-bound launch lists: id(plan) -> [plan, Program or None, refused]; `tape` collects
-        # the launches of the run that records one (every launch site appends while it is set)
-        self.replays: dict[int, list] = {}
+        # pre-bound launch lists: id(plan) -> [plan, Program or None, refused], least recently
+        # run first, at most replay.PLANS_KEPT; `tape` collects the launches of the run that
+        # records one (every launch site appends while it is set)
+        self.replays: collections.OrderedDict[int, list] = collections.OrderedDict()
         self.replay_graphs = True  # replay through a captured graph (False: launch by launch)
         self.tape: list[replay.Launch] | None = None
         self.issue_seconds = 0.0  # host time replayed runs spent before their barrier, summed
@@ -205,16 +207,27 @@ class HipDevice(CompiledDevice):
         a recording whose buffers overlap is refused and the plan keeps running call by call."""
         entry = self.replays.get(id(plan))
         if entry is None or entry[0] is not plan:
-            if entry is not None and entry[1] is not None:  # a dead plan's id, reused
-                self.finish()
-                entry[1].release(self.lib)
+            if entry is not None:  # a dead plan's id, reused
+                self._drop_replay(id(plan))
             self.replays[id(plan)] = [plan, None, False]
+            while len(self.replays) > replay.PLANS_KEPT:
+                self._drop_replay(next(iter(self.replays)))
             return super().run(plan, sources)
+        self.replays.move_to_end(id(plan))
         if entry[1] is not None:
             return self._replay(plan, entry[1], sources)
         if entry[2]:
             return super().run(plan, sources)
         return self._record(plan, sources, entry)
+
+    def _drop_replay(self, key: int) -> None:
+        """Forget one plan's launch list: its graphs are released once the device has finished
+        their launches; its arenas and staging buffers go back to the pool as their last
+        references drop (a result still held keeps its arena)."""
+        entry = self.replays.pop(key)
+        if entry[1] is not None:
+            self.finish()
+            entry[1].release(self.lib)
 
     def _record(self, plan, sources, entry: list):
         bufs: list = [None] * plan.positions
@@ -285,10 +298,7 @@ class HipDevice(CompiledDevice):
             slots[prog.positions + i] = out.ptr
         for i, p in prog.out_positions:
             bufs[p] = outs[i]
-        if self.replay_graphs:
-            check_limn(prog.launch_graph(self.lib, slots, self.finish))
-        else:
-            check_limn(prog.launch(self.lib, slots))
+        check_limn(prog.run(self.lib, slots, self.finish, self.replay_graphs))
         for p, i in prog.assigns:
             self.commit(sources[p], outs[i])
             bufs[p] = outs[i]

@@ -75,6 +75,7 @@ class Program:
     captures: int = 0  # graphs captured
     arenas: list = field(default_factory=list)  # the device's Arena objects for this list's outputs
     staging: dict = field(default_factory=dict)  # plan position -> the buffer host bytes are copied to
+    graph_failure: str | None = None  # why this list stopped using graphs, once it has
 
     @property
     def nslots(self) -> int:
@@ -100,6 +101,22 @@ class Program:
         return lib.limn_hip_replay_graph(self.steps.ctypes.data, len(self.steps), self.args.ctypes.data, len(self.args),
                                          slots.ctypes.data, len(slots), ctypes.byref(handle))
 
+    def run(self, lib, slots: np.ndarray, finish, graphs: bool) -> int:
+        """Issue the list for this binding: as a captured graph when `graphs` is set and no graph
+        of this list has failed, else launch by launch. A capture, instantiation or graph launch
+        that fails does so before any step runs (and the steps only write this replay's own
+        outputs), so the list then runs launch by launch, and keeps doing so: its graphs are
+        released and the reason kept in `graph_failure`. A list that cannot run launch by launch
+        either returns that status."""
+        if graphs and self.graph_failure is None:
+            status = self.launch_graph(lib, slots, finish)
+            if status == 0:
+                return 0
+            self.graph_failure = lib.limn_hip_last_error().decode() or f"status {status}"
+            finish()
+            self.release(lib)
+        return self.launch(lib, slots)
+
     def release(self, lib) -> None:
         """Free the captured graphs (after the device has finished every launch of them)."""
         for handle in self.graphs.values():
@@ -109,6 +126,7 @@ class Program:
 
 
 GRAPHS_PER_PLAN = 8
+PLANS_KEPT = 64  # launch lists a device keeps, the least recently run dropped first
 ARENAS_PER_PLAN = 3  # a list keeps this many output arenas; past that a replay takes a passing one
 ARENA_ALIGN = 256  # bytes between the starts of a replay's outputs in its arena
 
