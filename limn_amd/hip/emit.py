@@ -36,7 +36,7 @@ from __future__ import annotations
 import ctypes
 import math
 import re
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 
 import numpy as np
 
@@ -52,6 +52,8 @@ INTS = (int32, int16, int8)
 
 PRELUDE = r"""
 typedef long long i64;
+typedef unsigned short u16;
+typedef signed char i8;
 // every pointer a kernel takes is the start of a device allocation (views are index arithmetic),
 // so 16-byte runs along the stride-1 dim may be one vector access
 #define ALIGNED __attribute__((align_value(16)))
@@ -561,9 +563,111 @@ def prefetch_row(body: list[Instr], bufs: Buffers, var: str, vec: int, tag: str,
     return decls, loads, cached
 
 
+TRANSPOSE_TILE = 64  # a transposing nest's tile edge along each of its two variables
+ONE_WORD = {"unsigned short": "u16", "signed char": "i8"}  # storage types as one-word names
+TRANSPOSE_MIN_CELLS = 1 << 14  # the fewest output cells planned as tiles
+
+
+def transposed_loads(shape: NestShape, bufs: Buffers) -> tuple[str, list[Instr]] | None:
+    """The variable, and the loads, of an elementwise nest that reads across its output's rows:
+    plain loads contiguous along one variable `across` other than the output's stride-1 variable,
+    which they step by a stride above 1 (an optimizer reading a gradient realized transposed, a
+    contiguous copy of a transposed view). Read one cell per lane along the output's rows, each
+    such load touches a cache line per lane; `plan_transposed` reads them along `across`."""
+    write = shape.write
+    if write is None or write.opcode is not Opcode.STORE or len(shape.outer) < 2:
+        return None
+    inner, extent = shape.outer[-1]
+    if dict(write.arg[1].terms).get(inner) != 1 or extent < 16 or math.prod(e for _, e in shape.outer) < TRANSPOSE_MIN_CELLS:
+        return None
+    extents = dict(shape.outer)
+    across, found = None, []
+    for instr in shape.body:
+        if instr.opcode is not Opcode.LOAD:
+            continue
+        buf, index, _ = instr.arg
+        if buf in bufs.inline or buf in bufs.rowvals or instr.dest in bufs.cached:
+            continue
+        step = dict(index.terms).get(inner)
+        ones = [v for v, c in index.terms if c == 1 and v != inner and v in extents]
+        if step is None or step == 1 or not ones:
+            continue
+        if across not in (None, ones[0]):
+            return None
+        across = ones[0]
+        found.append(instr)
+    if across is None or extents[across] < 16:
+        return None
+    return across, found
+
+
+def plan_transposed(nest: LoopNest, shape: NestShape, bufs: Buffers, across: str, loads: list[Instr],
+                    stream: bool) -> Planned:
+    """An elementwise nest with loads contiguous along `across` (see transposed_loads), by tiles
+    of TRANSPOSE_TILE x TRANSPOSE_TILE cells over (`across`, the output's stride-1 variable), a
+    workgroup per tile, grid-strided: the lanes of a wave first read each such load along
+    `across` into an LDS tile (row pitch TILE+1 elements, so the transposed reads that follow hit
+    distinct banks), then compute and store a row of the output each, reading those loads from
+    the tile and every other load in place. The values are the ones the plain plan computes: the
+    same body, evaluated once per cell."""
+    T = TRANSPOSE_TILE
+    rows_per = THREADS // T
+    out_dtype = nest.kernel.target.dtype
+    write = shape.write
+    assert write is not None
+    inner, B = shape.outer[-1]
+    A = dict(shape.outer)[across]
+    rest = [(v, e) for v, e in shape.outer if v not in (inner, across)]
+    tiles = math.prod(e for _, e in rest) * -(-A // T) * -(-B // T)
+    wide = bufs.wide_index or math.prod(e for _, e in shape.outer) > (1 << 30)
+    lines = [signature(nest.name, nest, out_dtype, bufs) + " {", "  const i64 bid_ = blockIdx.x, nblk_ = gridDim.x;"]
+    refs = {}
+    for instr in loads:
+        st = ONE_WORD.get(STORE_T[bufs.dtypes[instr.arg[0]]], STORE_T[bufs.dtypes[instr.arg[0]]])
+        lines.append(f"  __shared__ {st} xt_{instr.dest}[{T * (T + 1)}];")
+        refs[instr.dest] = load_expr(bufs.dtypes[instr.arg[0]], f"xt_{instr.dest}[lb_ * {T + 1} + r_]")
+    lines.append(f"  const int lb_ = threadIdx.x & {T - 1};")
+    lines.append(f"  for (i64 tile_ = bid_; tile_ < {tiles}LL; tile_ += nblk_) {{")
+    lines += decode(rest + [("ta_", -(-A // T)), ("tb_", -(-B // T))], "tile_", "    ", wide)
+    lines.append("    {")
+    lines.append(f"      const int {across} = ta_ * {T} + lb_;")
+    lines.append("#pragma unroll 4")
+    lines.append(f"      for (int r_ = threadIdx.x / {T}; r_ < {T}; r_ += {rows_per}) {{")
+    lines.append(f"        const int {inner} = tb_ * {T} + r_;")
+    lines.append(f"        if ({across} < {A} && {inner} < {B}) {{")
+    for instr in loads:
+        buf, index, valid = instr.arg
+        st = STORE_T[bufs.dtypes[buf]]
+        ref = f"{buf}[{render_index(index, wide)}]"
+        if valid.bounds:
+            ref = f"({valid.render()}) ? {ref} : ({st})0"
+        lines.append(f"          xt_{instr.dest}[r_ * {T + 1} + lb_] = {ref};")
+    lines += ["        }", "      }", "    }", "    __syncthreads();"]
+    view = replace(bufs, cached={**bufs.cached, **refs})
+    lines.append(f"    const int {inner} = tb_ * {T} + lb_;")
+    lines.append("#pragma unroll 2")
+    lines.append(f"    for (int r_ = threadIdx.x / {T}; r_ < {T}; r_ += {rows_per}) {{")
+    lines.append(f"      const int {across} = ta_ * {T} + r_;")
+    lines.append(f"      if ({across} < {A} && {inner} < {B}) {{")
+    lines += ["        " + value_line(instr, view) for instr in shape.body]
+    buf, index = write.arg
+    lines.append(f"        {store_line(f'{buf}[{render_index(index, wide)}]', store_expr(out_dtype, write.srcs[0]), stream)}")
+    lines += ["      }", "    }", "    __syncthreads();", "  }", "}"]
+    grid = max(1, min(tiles, 1 << 20))
+    notes: dict = {"elementwise": True, "transposed": across, "body": lines[2:-1]}
+    notes["params"] = [(STORE_T[n.dtype], f"in{k}", True) for k, n in enumerate(nest.kernel.inputs)]
+    notes["params"] += [(STORE_T[bufs.dtypes[name]], name, True) for name in bufs.extra]
+    notes["params"].append((STORE_T[out_dtype], "out", False))
+    return Planned("\n".join(lines), [Launch(nest.name, grid, THREADS, "io")], notes=notes)
+
+
 def plan_elementwise(nest: LoopNest, shape: NestShape, bufs: Buffers, stream: bool = False) -> Planned:
     """One thread per run of `vec` output cells, grid-strided. With `stream`, the output goes
-    out through non-temporal stores (see STREAM_BYTES)."""
+    out through non-temporal stores (see STREAM_BYTES). A nest that reads across its output's
+    rows goes by tiles instead (see transposed_loads)."""
+    across = transposed_loads(shape, bufs)
+    if across is not None:
+        return plan_transposed(nest, shape, bufs, across[0], across[1], stream)
     cells = math.prod(e for _, e in shape.outer)
     write = shape.write
     assert write is not None
@@ -1371,19 +1475,80 @@ def add_epilogue(nest: LoopNest, total: Node, N: int) -> tuple[int, int | None] 
     return bias, res
 
 
-def epilogue_pairs(nests: list[LoopNest], plans: list[Planned], kept: set | None) -> tuple[dict[int, int], dict[int, tuple]]:
+def batch_sum_fold(reader: LoopNest, total: Node, con: Contraction) -> Contraction | None:
+    """The contraction a batched contraction and its reader make together when the reader only
+    sums the contraction's output over its batch: limn's weight gradient under a batched
+    activation (reference limn/tensor.py:486-496 spells a product as broadcast_to then
+    reshape/expand per operand, so a weight broadcast over the batch gets one product per batch
+    item, at the weight's dtype, and then a sum over the batch). Folded, the batch becomes part of
+    k (both operands must step through batch and k as one row-major index) and the result goes
+    straight to the reader's output, in its layout (the operands trade places when that layout has
+    the contraction's rows contiguous). One difference from the two nests: the per-item products
+    are not rounded to the operand dtype before the batch sum; every partial total stays in float
+    until the one rounding at the store."""
+    if con.batch <= 1 or con.a_batch != con.K * con.a_k or con.b_batch != con.K * con.b_k:
+        return None
+    shape = read_nest(reader)
+    if shape.fold is not Op.ADD or not shape.inner or len(shape.body) != 1 or shape.out_index.const != 0:
+        return None
+    load = shape.body[0]
+    if load.opcode is not Opcode.LOAD or load.dest != shape.item or load.arg[2].bounds or load.arg[1].const != 0:
+        return None
+    if reader.kernel.inputs[int(load.arg[0][2:])] is not total or reader.kernel.target.dtype != con.dtype:
+        return None
+    if shape.reduce_dtype != con.dtype or accumulate_in(con.dtype) is not float32 or con.c_m == con.c_n:
+        return None
+    terms, out_terms = dict(load.arg[1].terms), dict(shape.out_index.terms)
+    inner = [(v, e) for v, e in shape.inner if e > 1]
+    if math.prod(e for _, e in inner) != con.batch:
+        return None
+    order = sorted(inner, key=lambda ve: -terms.get(ve[0], 0))
+    if not order or terms.get(order[-1][0], 0) != con.c_batch:
+        return None
+    for (outer, _), (nxt, e) in zip(order, order[1:]):
+        if terms.get(outer, 0) != e * terms.get(nxt, 0):
+            return None
+    rows = cols = None
+    for v, e in shape.outer:
+        if e == 1:
+            continue
+        if terms.get(v) == con.c_m and e == con.M and rows is None:
+            rows = out_terms.get(v, 0)
+        elif terms.get(v) == con.c_n and e == con.N and cols is None:
+            cols = out_terms.get(v, 0)
+        else:
+            return None
+    if not rows or not cols:
+        return None
+    K = con.batch * con.K
+    if cols == 1 or rows != 1:
+        folded = replace(con, batch=1, K=K, a_batch=0, b_batch=0, c_batch=0, c_m=rows, c_n=cols)
+    else:  # the reader's rows are the contraction's columns: c^T = b^T a^T, rows contiguous
+        folded = Contraction(con.b_input, con.a_input, con.b_offset, con.a_offset, con.dtype, 1, con.N, con.M, K,
+                             0, con.b_n, con.b_k, 0, con.a_k, con.a_m, 0, cols, rows)
+    from limn_amd.dtypes import ABI_CODE
+
+    lib = runtime.kernels()
+    ok = lib.limn_hip_matmul_supported(ABI_CODE[folded.dtype], folded.M, folded.N, folded.K, 0, folded.a_m, folded.a_k, 0,
+                                       folded.b_k, folded.b_n)
+    return folded if ok else None
+
+
+def epilogue_pairs(nests: list[LoopNest], plans: list[Planned], kept: set | None) -> tuple[dict[int, int], dict[int, tuple], dict[int, Contraction]]:
     """Readers to run as their contraction's epilogue: ({contraction nest: reader nest}, {reader
     nest: (bias input, residual input or None, the bias's cast nest or None)} for the readers that
-    add terms, see add_epilogue and bias_cast; the others are relu nests).
+    add terms, see add_epilogue and bias_cast; {reader nest: folded contraction} for the readers
+    that sum a batched contraction over its batch, see batch_sum_fold; the others are relu nests).
 
     The reader crosses a scheduler cut (the SUM is its own kernel), so it may only move into the
     contraction's store when nothing else needs the SUM's buffer: the reader is its only reader
     among the plan's nests, and it is neither a sink nor read by a CUSTOM call (`kept`, recorded
     by the device's plan_of; None when unknown, which fuses nothing)."""
     if kept is None:
-        return {}, {}
+        return {}, {}, {}
     pairs: dict[int, int] = {}
     addends: dict[int, tuple] = {}
+    folds: dict[int, Contraction] = {}
     for i, plan in enumerate(plans):
         con = plan.contraction
         if con is None:
@@ -1404,7 +1569,12 @@ def epilogue_pairs(nests: list[LoopNest], plans: list[Planned], kept: set | None
         if terms is not None and math.prod(out.shape) == math.prod(total.shape):
             pairs[i] = j
             addends[j] = (*terms, bias_cast(nests, nests[j].kernel.inputs[terms[0]], j, kept))
-    return pairs, addends
+            continue
+        folded = batch_sum_fold(nests[j], total, con)
+        if folded is not None:
+            pairs[i] = j
+            folds[j] = folded
+    return pairs, addends, folds
 
 
 def bias_cast(nests: list[LoopNest], bias: Node, reader: int, kept: set) -> int | None:
@@ -1653,13 +1823,26 @@ def merge_runs(nests: list[LoopNest], plans: list[Planned], custom_inputs: set |
 
 def merged_source(name: str, nests: list[LoopNest], plans: list[Planned], run: list[int]) -> tuple[str, int]:
     """One kernel for a run of elementwise nests: each member's body in its own block range, its
-    buffer names bound to its own parameters."""
+    buffer names bound to its own parameters. A workgroup runs one member, so the members' LDS
+    arrays (a transposing member's tiles) all start at the kernel's one `mshared_`."""
     params: list[str] = []
     segments: list[str] = []
     offset = 0
+    lds = 0
     for s_, c in enumerate(run):
         plan = plans[c]
         grid = plan.launches[0].grid
+        at = 0
+
+        def shared(d) -> str:
+            nonlocal at
+            t, var, dims = d.group(1), d.group(2), [int(x) for x in re.findall(r"\d+", d.group(3))]
+            start = -(-at // 16) * 16
+            at = start + math.prod(dims) * _SIZES[t]
+            return f"{t}* {var} = ({t}*)(mshared_ + {start});"
+
+        body = [_SHARED.sub(shared, ln) for ln in plan.notes["body"]]
+        lds = max(lds, at)
         binds = []
         for ctype, pname, const in plan.notes["params"]:
             q = "const " if const else ""
@@ -1670,9 +1853,11 @@ def merged_source(name: str, nests: list[LoopNest], plans: list[Planned], run: l
         segments.append(f"{head} ({cond}) {{" if s_ < len(run) - 1 else ("  } else {" if s_ else "  {"))
         segments += binds
         segments.append(f"    const i64 bid_ = (i64)blockIdx.x - {offset}, nblk_ = {grid};")
-        segments += ["  " + ln for ln in plan.notes["body"]]
+        segments += ["  " + ln for ln in body]
         offset += grid
     segments.append("  }")
+    if lds:
+        segments.insert(0, f"  __shared__ __attribute__((aligned(16))) char mshared_[{lds}];")
     source = f'extern "C" __global__ __launch_bounds__({THREADS}) void {name}({", ".join(params)}) {{\n' + "\n".join(segments) + "\n}"
     return source, offset
 
@@ -1682,7 +1867,7 @@ _KERNEL_HEAD = re.compile(r'extern "C" __global__ __launch_bounds__\(\d+\) void 
 
 
 _SHARED = re.compile(r"__shared__ (\w+) (\w+)((?:\[\d+\])+);")
-_SIZES = {"float": 4, "double": 8, "int": 4, "i64": 8, "short": 2, "char": 1}
+_SIZES = {"float": 4, "double": 8, "int": 4, "i64": 8, "short": 2, "u16": 2, "i8": 1, "char": 1}
 
 
 def as_device_function(source: str, grid: int) -> tuple[str, str, list[str], int]:
@@ -2216,6 +2401,9 @@ class Program:
     # input or None, the nest whose float32 input the epilogue rounds into the bias, or None)};
     # the other epilogues are relus
     addends: dict[int, tuple] = field(default_factory=dict)
+    # the epilogue readers that sum a batched contraction over its batch: {reader nest: the
+    # contraction with the batch folded into k, into the reader's output}
+    folds: dict[int, "Contraction"] = field(default_factory=dict)
 
     def launcher_of(self, key: int) -> int:
         return self.launch_at.get(key, key)
@@ -2252,10 +2440,12 @@ def plan_program(nests: list[LoopNest], kept: set | None, custom_inputs: set | N
     Touches no GPU."""
     streamed = streamed_outputs(nests, kept, custom_inputs)
     plans = [plan_nest(n, stream=k in streamed) for k, n in enumerate(nests)]
-    pairs, addends = epilogue_pairs(nests, plans, kept)
+    pairs, addends, folds = epilogue_pairs(nests, plans, kept)
     fused = {j: i for i, j in pairs.items()}
     for j in fused:
         plans[j] = Planned("", [], notes={"epilogue of": nests[fused[j]].name})
+        if j in folds:
+            plans[j].notes["batch folded into k"] = True
     absorbed = {terms[2] for terms in addends.values() if terms[2] is not None}
     inlined = InlineSet(nests, inline_producers(nests, plans, kept, pairs) | absorbed)
     for c, nest in enumerate(nests):
@@ -2292,7 +2482,7 @@ def plan_program(nests: list[LoopNest], kept: set | None, custom_inputs: set | N
     names += [fold.name for fold, _, _ in columns.values()]
     kept_sources = [p.source for k, p in enumerate(plans) if k not in in_run]
     source = PRELUDE + "\n".join(kept_sources + merged_sources) if names else ""
-    return Program(plans, pairs, inlined, merged, source, names, launch_at, columns, addends)
+    return Program(plans, pairs, inlined, merged, source, names, launch_at, columns, addends, folds)
 
 
 def nest_runners(dev, nests: list[LoopNest]):
@@ -2330,6 +2520,9 @@ def nest_runners(dev, nests: list[LoopNest]):
             runners.append(_merged_runner(dev, launches, nests, inlined, producer_inputs, deferred, k))
         elif role == "deferred":
             runners.append(_defer_runner(deferred, k))
+        elif role == "epilogue" and k in prog.folds:
+            source = next(i for i, j in pairs.items() if j == k)
+            runners.append(_fold_runner(dev, prog.folds[k], operands, source))
         elif role == "epilogue":
             source = next(i for i, j in pairs.items() if j == k)
             runners.append(_epilogue_runner(dev, plans[source].contraction, operands, source, prog.addends.get(k),
@@ -2461,6 +2654,18 @@ def _stash_runner(operands: dict, k: int):
         operands[k] = inputs
 
     run.launches_nothing = True
+    return run
+
+
+def _fold_runner(dev, folded: Contraction, operands: dict, k: int):
+    """The batch-sum reader's call: the batched contraction of nest k with its batch folded into
+    k, stored into this nest's output (see batch_sum_fold)."""
+    launch = _matmul_launcher(dev, folded, 0)
+
+    def run(inputs: list, outs: list) -> None:
+        launch(operands.pop(k), outs[0].ptr)
+
+    run.folded = folded
     return run
 
 

@@ -432,18 +432,20 @@ class Tensor:
     # ---- composed ----
 
     def matmul(self, other: Tensor) -> Tensor:
+        """The product as limn spells it (reference limn/tensor.py:486-496): each operand
+        broadcast to the batch shape, then reshaped and expanded over the other's rows, then one
+        sum over k. Its backward follows the same views back: an operand that was broadcast over
+        the batch (a weight under a batched activation) gets a batched contraction over the rows
+        (one product per batch, at the operand's dtype) and then a sum over the batch."""
         if self.ndim < 2 or other.ndim < 2:
             raise ValueError(f"matmul needs 2D+ tensors, got {self.shape} @ {other.shape}")
         (m, k), (k2, n) = self.shape[-2:], other.shape[-2:]
         if k != k2:
             raise ValueError(f"matmul: inner dims differ, {self.shape} @ {other.shape}")
         batch = _broadcast_shape(self.shape[:-2], other.shape[:-2], "matmul")
-
-        def lifted(t: Tensor, rows: tuple[int, int]) -> Tensor:
-            ones = (1,) * (len(batch) + 2 - t.ndim)
-            return t.reshape(*ones, *t.shape[:-2], *rows, k).expand(*batch, m, n, k)
-
-        return (lifted(self, (m, 1)) * lifted(other.transpose(-2, -1), (1, n))).sum(axis=-1)
+        a = _broadcast(self, batch + (m, k), "matmul").reshape(*batch, m, 1, k).expand(*batch, m, n, k)
+        b = _broadcast(other, batch + (k, n), "matmul").transpose(-2, -1).reshape(*batch, 1, n, k).expand(*batch, m, n, k)
+        return (a * b).sum(axis=-1)
 
     __matmul__ = matmul
 

@@ -11,7 +11,7 @@ import math
 import numpy as np
 import pytest
 
-from limn_amd.seam import bfloat16, float32, lower_all, Op, realized, schedule, Tensor, topological
+from limn_amd.seam import bfloat16, float32, grad, lower_all, Op, realized, schedule, Tensor, topological
 from limn_amd.seam import device as limn_device
 
 emit = pytest.importorskip("limn_amd.hip.emit")
@@ -90,13 +90,13 @@ def test_no_fusion_when_a_custom_call_reads_the_sum():
     nests, kept = lowered([out])
     plans = [emit.plan_nest(n) for n in nests]
     assert any(p.contraction is not None for p in plans)
-    assert emit.epilogue_pairs(nests, plans, kept) == ({}, {})
+    assert emit.epilogue_pairs(nests, plans, kept) == ({}, {}, {})
 
 
 def test_no_fusion_without_a_record_of_readers():
     a, b = operands()
     nests, _ = lowered([(a @ b).relu()])
-    assert emit.epilogue_pairs(nests, [emit.plan_nest(n) for n in nests], None) == ({}, {})
+    assert emit.epilogue_pairs(nests, [emit.plan_nest(n) for n in nests], None) == ({}, {}, {})
 
 
 def bias_operands(m: int = 64, k: int = 64, n: int = 48):
@@ -123,14 +123,14 @@ def test_a_cast_bias_is_rounded_by_the_epilogue():
     w = Tensor(rng.standard_normal(48).astype(np.float32), dtype=float32)
     nests, kept = lowered([a @ b + w.cast(bfloat16)])
     plans = [emit.plan_nest(n) for n in nests]
-    pairs, addends = emit.epilogue_pairs(nests, plans, kept)
+    pairs, addends, _ = emit.epilogue_pairs(nests, plans, kept)
     ((j, (bias, res, cast)),) = addends.items()
     assert cast is not None and nests[cast].kernel.target is nests[j].kernel.inputs[bias]
     prog = emit.plan_program(nests, kept, set())
     assert prog.role(cast) == "inlined" and not prog.plans[cast].launches
     wb = w.cast(bfloat16)
     nests, kept = lowered([a @ b + wb, wb * 2.0])
-    _, addends = emit.epilogue_pairs(nests, [emit.plan_nest(n) for n in nests], kept)
+    _, addends, _ = emit.epilogue_pairs(nests, [emit.plan_nest(n) for n in nests], kept)
     assert [t[2] for t in addends.values()] == [None]
 
 
@@ -336,6 +336,78 @@ def test_merged_kernel_binds_each_members_buffers():
     source, grid = emit.merged_source("merged", nests, plans, runs[0])
     assert grid == sum(plans[c].launches[0].grid for c in runs[0])
     assert "s0_in0" in source and "s1_out" in source and source.count("const i64 bid_") == 2
+
+
+def test_a_read_across_the_output_rows_is_planned_by_tiles():
+    """A gradient realized transposed, read by an optimizer's update: the load is contiguous
+    along the output's row variable, so the nest goes by LDS tiles; a nest reading along the
+    output's rows keeps the plain plan. Both compile (hipRTC needs no GPU)."""
+    from limn_amd.hip import runtime
+
+    g = Tensor(rng.standard_normal((200, 300)).astype(np.float32), dtype=bfloat16)
+    m = Tensor(rng.standard_normal((300, 200)).astype(np.float32))
+    nests, _ = lowered([m * 0.9 + g.transpose().cast(float32) * 0.1])
+    tiled = emit.plan_nest(nests[0])
+    assert tiled.notes.get("transposed") == "i0" and tiled.launches[0].grid == 4 * 5
+    assert "__syncthreads" in tiled.source and "xt_" in tiled.source
+    runtime.compile_source(emit.PRELUDE + tiled.source, [tiled.launches[0].name])
+    nests, _ = lowered([m * 0.9 + g.transpose().transpose().transpose().cast(float32)])
+    assert emit.plan_nest(nests[0]).notes.get("transposed") == "i0"
+    nests, _ = lowered([m * 2.0 + 1.0])
+    assert "transposed" not in emit.plan_nest(nests[0]).notes
+
+
+def test_small_or_narrow_transposes_keep_the_plain_plan():
+    """Below TRANSPOSE_MIN_CELLS cells, or with a side under 16, a tile would be mostly empty."""
+    small = Tensor(rng.standard_normal((20, 30)).astype(np.float32))
+    narrow = Tensor(rng.standard_normal((8, 4000)).astype(np.float32))
+    for t in (small, narrow):
+        nests, _ = lowered([t.transpose() * 2.0])
+        assert "transposed" not in emit.plan_nest(nests[0]).notes
+
+
+def test_transposing_members_of_a_merged_launch_share_one_lds_pool():
+    """Moment updates of three matrices whose gradients arrive transposed merge into one launch;
+    each member's tile becomes a pointer into the kernel's one LDS array, sized for the largest
+    member, and the merged kernel compiles."""
+    from limn_amd.hip import runtime
+
+    shapes = [(200, 300), (96, 640), (512, 129)]
+    moms = [Tensor(rng.standard_normal(sh).astype(np.float32)) for sh in shapes]
+    grads = [Tensor(rng.standard_normal(sh[::-1]).astype(np.float32), dtype=bfloat16) for sh in shapes]
+    nests, runs = runs_of([m * 0.9 + g.transpose().cast(float32) * 0.1 for m, g in zip(moms, grads)])
+    assert [len(r) for r in runs] == [3]
+    plans = [emit.plan_nest(n) for n in nests]
+    assert all(plans[c].notes.get("transposed") for c in runs[0])
+    source, grid = emit.merged_source("merged", nests, plans, runs[0])
+    assert source.count("__shared__") == 1 and source.count("(mshared_ + 0)") == 3
+    assert f"char mshared_[{64 * 65 * 2}]" in source
+    runtime.compile_source(emit.PRELUDE + source, ["merged"])
+
+
+def test_limn_spelled_weight_gradient_folds_the_batch_into_k():
+    """limn's matmul broadcasts both operands to (batch, m, n, k) and sums k (reference
+    limn/tensor.py:486-496). The gradient of a weight shared over the batch is then a batched
+    contraction, a product per batch entry, and a sum over the batch: the emitter runs the two as
+    one contraction with the batch folded into k, launched by the sum's runner (the batched
+    products are never stored), and the optimizer-side read of that gradient, transposed, goes
+    by tiles."""
+    x = Tensor(rng.standard_normal((8, 64, 96)).astype(np.float32), dtype=bfloat16, requires_grad=True)
+    w = Tensor(rng.standard_normal((256, 96)).astype(np.float32), dtype=bfloat16, requires_grad=True)
+    y = x @ w.transpose()
+    loss = (y.cast(float32) * Tensor(rng.standard_normal((8, 64, 256)).astype(np.float32))).sum()
+    gx, gw = grad(loss, [x, w])
+    update = Tensor(np.zeros((256, 96), np.float32)) * 0.9 + gw.cast(float32) * 0.1
+    nests, kept = lowered([gx, update])
+    prog = emit.plan_program(nests, kept, set())
+    assert len(prog.folds) == 1
+    (k, folded), = prog.folds.items()
+    batched = next(c for c, j in prog.pairs.items() if j == k)
+    assert prog.plans[batched].contraction.batch == 8
+    assert folded.batch == 1 and folded.K == 8 * 64 and {folded.M, folded.N} == {96, 256}
+    assert prog.role(batched) == "stash" and prog.role(k) == "epilogue"
+    assert prog.plans[k].notes.get("batch folded into k")
+    assert any(p.notes.get("transposed") for p in prog.plans)
 
 
 def test_a_large_sink_streams_its_stores():

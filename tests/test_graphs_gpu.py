@@ -10,6 +10,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
+from conftest import storage_values
 from graphs import GRAPHS, check
 from limn_amd.seam import bfloat16, float16, float32, float64, grad, int16, int32, int8, Op, Tensor, topological
 from limn_amd.seam import device as limn_device
@@ -328,6 +329,99 @@ def test_commits_of_a_batch_run_as_one_copy(hipdev):
         np.testing.assert_array_equal(hipdev.copyout(t), w)
 
 
+TRANSPOSED = {
+    "bf16-cast-add": (lambda g, m: m * 0.9 + g.transpose().cast(float32) * 0.1, (300, 200), bfloat16),
+    "batched-f32": (lambda g, m: g.transpose() * m, (3, 70, 130), float32),
+    "outer-dims-swapped": (lambda g, m: g.permute(2, 1, 0) + m, (60, 3, 130), float32),
+    "padded": (lambda g, m: g.transpose().pad(((1, 2), (0, 3))), (97, 180), float32),
+    "optimizer-shape": (lambda g, m: m * 0.999 + (g.transpose().cast(float32) * g.transpose().cast(float32)) * 0.001, (1536, 512), bfloat16),
+    "int32": (lambda g, m: g.transpose() * 3, (130, 129), int32),
+}
+
+
+@pytest.mark.parametrize("name", list(TRANSPOSED))
+def test_reads_across_the_output_rows_go_by_tiles(hipdev, name):
+    """Elementwise nests whose loads are contiguous along another variable than the output's
+    (a gradient realized transposed, as an optimizer reads it): the plan stages those loads
+    through LDS tiles (checked on the emitter's plan), and the values are numpy's: the copies
+    bit for bit, the arithmetic to float32 rounding."""
+    from limn_amd.hip import emit
+    from limn_amd.seam import lower_all, schedule
+
+    spell, out_shape, dtype = TRANSPOSED[name]
+    src_shape = tuple(reversed(out_shape)) if name == "outer-dims-swapped" else out_shape[:-2] + out_shape[:-3:-1]
+    if dtype is int32:
+        g = Tensor(rng.integers(-1000, 1000, src_shape).astype(np.int32))
+    else:
+        g = Tensor(randf(*src_shape), dtype=dtype)
+    m = Tensor(randf(*out_shape))
+    y = spell(g, m)
+    nodes = [y.node]
+    order = topological(nodes)
+    nests = lower_all(nodes, order, schedule(nodes, order))
+    assert any(emit.plan_nest(n).notes.get("transposed") for n in nests)
+    exact = name in ("padded", "int32")
+    check(hipdev, y, bitwise=exact, rtol=1e-6, atol=1e-6)
+
+
+def test_transposed_gradients_in_merged_optimizer_launches(hipdev):
+    """Moments and parameters of several matrices whose gradients arrive transposed: the
+    transposing members share merged launches (their LDS tiles from one pool), and every
+    committed value matches numpy."""
+    limn_device.active_device = hipdev
+    shapes = [(200, 300), (96, 64), (512, 129)]
+    ps = [Tensor(randf(*sh)) for sh in shapes]
+    ms = [Tensor(randf(*sh)) for sh in shapes]
+    g_raw = [randf(*sh[::-1]) for sh in shapes]
+    gs = [Tensor(g, dtype=bfloat16) for g in g_raw]
+    p_old, m_old = ([t.numpy().copy() for t in ts] for ts in (ps, ms))
+    g_np = [storage_values(g, bfloat16) for g in g_raw]
+    sinks = []
+    for p, m, g in zip(ps, ms, gs):
+        m_new = m * 0.9 + g.transpose().cast(float32) * 0.1
+        m.assign(m_new)
+        p.assign(p - m_new * 0.01)
+        sinks += [m.node, p.node]
+    bufs = hipdev.execute(sinks)
+    for k in range(len(shapes)):
+        want_m = m_old[k] * np.float32(0.9) + g_np[k].T * np.float32(0.1)
+        got_m = hipdev.copyout(bufs[2 * k]).view(np.float32).reshape(shapes[k])
+        got_p = hipdev.copyout(bufs[2 * k + 1]).view(np.float32).reshape(shapes[k])
+        np.testing.assert_allclose(got_m, want_m, rtol=1e-6, atol=1e-6)
+        np.testing.assert_allclose(got_p, p_old[k] - want_m * np.float32(0.01), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("batch", [1, 8], ids=["unbatched", "batched"])
+def test_matmul_forward_and_backward_in_limns_spelling(hipdev, batch):
+    """x @ w.T for x (batch, m, k) and a weight w (n, k) shared over the batch, spelled as limn
+    spells matmul: both operands broadcast to (batch, m, n, k), then a sum over k (reference
+    limn/tensor.py:486-496, 806-812). The output and both gradients match the oracle's. For a
+    batch above 1 the weight's gradient is a batched contraction and a sum over the batch, which
+    the device runs as one contraction with the batch folded into k (checked on the recorded
+    plan): it rounds to bfloat16 once where the oracle rounds every batch entry's product first,
+    so the bound there is on the worst error over the largest magnitude."""
+    m, k, n = 64, 96, 256
+    xd = rng.standard_normal((batch, m, k)).astype(np.float32)
+    wd = rng.standard_normal((n, k)).astype(np.float32)
+    x = Tensor(xd, dtype=bfloat16, requires_grad=True)
+    w = Tensor(wd, dtype=bfloat16, requires_grad=True)
+    y = x @ w.transpose()
+    loss = (y.cast(float32) * Tensor(randf(batch, m, n))).sum()
+    gx, gw = grad(loss, [x, w])
+    check(hipdev, y, worst=1e-2)  # one bfloat16 rounding of sums taken in another order
+    check(hipdev, gx, worst=1e-2)
+    hipdev.record = []
+    try:
+        hipdev.execute([gw.node])
+        plan = hipdev.record[0].plan
+    finally:
+        hipdev.record = None
+    folded = [call.fn.folded for call in plan.calls if hasattr(call.fn, "folded")]
+    if batch > 1:
+        assert len(folded) == 1 and folded[0].batch == 1 and folded[0].K == batch * m
+    check(hipdev, gw, worst=1e-2)
+
+
 def test_optimizer_style_updates_in_merged_launches(hipdev):
     """Moments then parameters for several parameters, the way an optimizer step writes them:
     the device launches each group of independent updates as one kernel (checked through the
@@ -636,7 +730,7 @@ def test_bias_epilogue_matches_the_separate_add_bit_for_bit(hipdev, m, n, k, res
     nodes = [out.node]
     order = topological(nodes)
     nests = lower_all(nodes, order, schedule(nodes, order))
-    _, addends = emit.epilogue_pairs(nests, [emit.plan_nest(x) for x in nests], {realized(x) for x in nodes})
+    _, addends, _ = emit.epilogue_pairs(nests, [emit.plan_nest(x) for x in nests], {realized(x) for x in nodes})
     assert addends, "the add did not become the contraction's epilogue"
     fused = hipdev.copyout(hipdev.execute([out.node])[0]).view(np.uint16)
     _, separate = hipdev.execute([mm.node, out.node])
@@ -648,11 +742,13 @@ def test_bias_epilogue_matches_the_separate_add_bit_for_bit(hipdev, m, n, k, res
 
 def test_weight_gradient_is_one_split_k_contraction(hipdev):
     """A weight gradient sums over batch and rows together (K = 8 * 512 = 4096) into a 256 x 128
-    output: one contraction, split in k (the output is two 128-tiles), its slices added in order.
-    Checked against the float64 closed form on the same bf16 values and the float32 total rounded
-    once at the store."""
+    output. limn's matmul spelling makes it a product per batch entry and a sum over the batch;
+    the device runs the two as one contraction with the batch folded into k, split in k (the
+    output is two 128-tiles), its slices added in order. Checked against the float64 closed form
+    on the same bf16 values and the float32 total rounded once at the store."""
     from limn_amd.dtypes import bf16_bits, bf16_values
-    from limn_amd.hip import runtime
+    from limn_amd.hip import emit, runtime
+    from limn_amd.seam import lower_all, realized
 
     B, T, C, O = 8, 512, 128, 256
     x_vals = bf16_values(bf16_bits(rng.standard_normal((B, T, C)).astype(np.float32)))
@@ -661,8 +757,8 @@ def test_weight_gradient_is_one_split_k_contraction(hipdev):
     x, dy = Tensor(x_vals, dtype=bfloat16), Tensor(dy_vals, dtype=bfloat16)
     w = Tensor(np.zeros((O, C), np.float32), requires_grad=True)
     (gw,) = grad((x @ w.cast(bfloat16).transpose() * dy).sum(), [w])
-    plans = _plans(hipdev, gw)
-    cons = [p.contraction for p in plans if p.contraction is not None]
+    prog = emit.plan_program(lower_all([gw.node]), {realized(gw.node)}, set())
+    cons = [p.contraction for p in prog.plans if p.contraction is not None] + list(prog.folds.values())
     wgrad = [c for c in cons if c.K == B * T]
     assert wgrad, f"no contraction over batch and rows: {[(c.M, c.N, c.K) for c in cons]}"
     c = wgrad[0]
