@@ -700,7 +700,8 @@ def bench_c5(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
         "unit": "tok/s",
         "ms_per_step": round(elapsed / steps * 1e3, 3),
         "dtype": "bf16",
-        "config": {"workload": "C5 byte-level GPT training step (captured), d512 L8 H8 ctx512 batch32, AdamW",
+        "config": {"workload": "C5 byte-level GPT training step (captured), d512 L8 H8 ctx512 batch32, AdamW; "
+                               "matmul in limn spelling (both operands broadcast to (batch, m, n, k), summed over k)",
                    "tokens_per_step": cfg.tokens, "flop_per_step": per_step, "params_in_matmuls": cfg.matmul_params()},
         "mfu": round(per_step * steps / elapsed / MFMA_BF16_PEAK, 4),
         "loss": {"after_warmup": round(first_loss, 4), "last": round(last_loss, 4)},
