@@ -83,7 +83,9 @@ def build(force: bool = False, verbose: bool = False) -> Path:
                     print(f"hipcc {src.name}", flush=True)
             list(pool.map(lambda job: _compile(*job), todo))
     tmp = LIBRARY.with_suffix(".so.tmp")
-    cmd = [hipcc(), *FLAGS, "-shared", "-o", str(tmp), *(str(o) for _, o in jobs)]
+    # every symbol resolved at link time: a kernel whose launch stub the host pass did not emit
+    # would otherwise surface only when the library is loaded on the GPU box
+    cmd = [hipcc(), *FLAGS, "-shared", "-Wl,--no-undefined", "-o", str(tmp), *(str(o) for _, o in jobs)]
     done = subprocess.run(cmd, capture_output=True, text=True)
     if done.returncode != 0:
         raise RuntimeError(f"linking liblimn_hip.so failed:\n{done.stderr[-8000:]}")
