@@ -234,6 +234,31 @@ def copy_probe(steps: int) -> int:
     return 0
 
 
+def launch_floor_us(dev, launches: int, steps: int) -> float:
+    """Microseconds per step of `launches` back-to-back launches that do nothing (the copy probe
+    with no elements, 32 workgroups, as many as C1's forward): the floor of a step made of that
+    many dependent launches on an idle GPU."""
+    from limn_amd.hip import runtime
+
+    fn = runtime.load_functions(COPY_SOURCE, ["limn_copy_probe"])["limn_copy_probe"]
+    n, a, b = ctypes.c_longlong(0), ctypes.c_void_p(0), ctypes.c_void_p(0)
+    params = (ctypes.c_void_p * 3)(ctypes.addressof(a), ctypes.addressof(b), ctypes.addressof(n))
+
+    def step() -> None:
+        for _ in range(launches):
+            runtime.check(dev.api.hipModuleLaunchKernel(fn, 32, 1, 1, 256, 1, 1, 0, None, params, None), "launching an empty kernel")
+
+    step()
+    dev.finish()
+    ev = Events(dev.api, 2)
+    ev.record(0)
+    for _ in range(steps):
+        step()
+    ev.record(1)
+    dev.finish()
+    return ev.ms(0, 1) / steps * 1e3
+
+
 class NoEvents:
     """An Events stand-in that records nothing."""
 
@@ -604,6 +629,7 @@ def bench_c1(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     dev.finish()
     us = ev.ms(0, 1) / steps * 1e3
     flops = 7 * (2.0 * B * H * S * S * D / 2)  # 2.35e8: fwd 2U + bwd 5U, causal counted as half
+    floor_us = launch_floor_us(dev, 3, steps)
 
     def build():
         Q, K, V = (Tensor(x, requires_grad=True) for x in host[:3])
@@ -619,7 +645,8 @@ def bench_c1(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
         "dtype": "f32",
         "config": {"workload": "C1 causal sdpa f32 B2 H4 S256 D64, fwd + bwd (general-width kernels)", "flop_per_step": flops},
         "tflops": round(flops / (us * 1e-6) / 1e12, 3),
-        "roofline": {"kernel": "sdpa (all three passes)", "bound": "latency", "achieved": round(flops / (us * 1e-6) / 1e12, 3),
+        "launch_floor_us": round(floor_us, 2),
+        "roofline": {"kernel": "sdpa (all three passes)", "bound": "latency", "floor_us": round(floor_us, 2), "achieved": round(flops / (us * 1e-6) / 1e12, 3),
                      "peak": 157.3, "unit": "TFLOP/s", "frac": round(flops / (us * 1e-6) / 157.3e12, 5), "traffic": None},
         "cpu_baseline": None if cpu_s is None else {
             "value": round(cpu_s * 1e6, 1),
