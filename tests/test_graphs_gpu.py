@@ -391,20 +391,22 @@ def test_transposed_gradients_in_merged_optimizer_launches(hipdev):
         np.testing.assert_allclose(got_p, p_old[k] - want_m * np.float32(0.01), rtol=1e-6, atol=1e-6)
 
 
-@pytest.mark.parametrize("batch", [1, 8], ids=["unbatched", "batched"])
-def test_matmul_forward_and_backward_in_limns_spelling(hipdev, batch):
+@pytest.mark.parametrize("batch,m,k,n,dtype", [(1, 64, 96, 256, bfloat16), (8, 64, 96, 256, bfloat16),
+                                               (3, 50, 70, 36, bfloat16), (4, 64, 128, 192, float16)],
+                         ids=["unbatched", "batched", "ragged", "float16"])
+def test_matmul_forward_and_backward_in_limns_spelling(hipdev, batch, m, k, n, dtype):
     """x @ w.T for x (batch, m, k) and a weight w (n, k) shared over the batch, spelled as limn
     spells matmul: both operands broadcast to (batch, m, n, k), then a sum over k (reference
     limn/tensor.py:486-496, 806-812). The output and both gradients match the oracle's. For a
     batch above 1 the weight's gradient is a batched contraction and a sum over the batch, which
     the device runs as one contraction with the batch folded into k (checked on the recorded
     plan): it rounds to bfloat16 once where the oracle rounds every batch entry's product first,
-    so the bound there is on the worst error over the largest magnitude."""
-    m, k, n = 64, 96, 256
+    so the bound there is on the worst error over the largest magnitude. A ragged shape (rows not
+    a multiple of 8) runs the products as ordinary reduces instead."""
     xd = rng.standard_normal((batch, m, k)).astype(np.float32)
     wd = rng.standard_normal((n, k)).astype(np.float32)
-    x = Tensor(xd, dtype=bfloat16, requires_grad=True)
-    w = Tensor(wd, dtype=bfloat16, requires_grad=True)
+    x = Tensor(xd, dtype=dtype, requires_grad=True)
+    w = Tensor(wd, dtype=dtype, requires_grad=True)
     y = x @ w.transpose()
     loss = (y.cast(float32) * Tensor(randf(batch, m, n))).sum()
     gx, gw = grad(loss, [x, w])
@@ -417,7 +419,7 @@ def test_matmul_forward_and_backward_in_limns_spelling(hipdev, batch):
     finally:
         hipdev.record = None
     folded = [call.fn.folded for call in plan.calls if hasattr(call.fn, "folded")]
-    if batch > 1:
+    if batch > 1 and m % 8 == 0:  # the MFMA contraction takes k in multiples of 8
         assert len(folded) == 1 and folded[0].batch == 1 and folded[0].K == batch * m
     check(hipdev, gw, worst=1e-2)
 
