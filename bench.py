@@ -891,7 +891,7 @@ def main() -> int:
     # the template instance each CUSTOM name runs at this configuration (rocprofv3's kernel names)
     KERNEL_SYMBOL = {
         "sdpa": "sdpa_fwd_dma<BF16,true,false>",
-        "sdpa_bwd_kv": "sdpa_bwd_kv_piped<BF16,true,true>",
+        "sdpa_bwd_kv": "sdpa_bwd_kv_dual<BF16,true,true>",
         "sdpa_bwd_q": "sdpa_dq_ds<BF16,true>",
     }
     dom = int(np.argmax(per))

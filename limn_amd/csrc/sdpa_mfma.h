@@ -3,7 +3,8 @@
 // three CUSTOM kernels limn's attention seam asks for (reference limn/tensor.py:509-575,
 // 679-714), each deterministic: every total is accumulated inside one wave in a fixed order.
 //
-// Work decomposition (all three kernels):
+// Work decomposition (all three kernels; the unmasked D = 128 dK/dV pass differs, see
+// sdpa_bwd_kv_dual):
 //   a workgroup is 4 waves and owns 128 * NT *resident* rows (queries for the forward and dQ
 //   pass, keys for the dK/dV pass), NT tiles of 32 per wave; the other side *streams* past in
 //   tiles of TILE = 64 rows staged through LDS (the next tile's global loads in flight while the
@@ -790,10 +791,11 @@ __global__ __launch_bounds__(THREADS, NT == 1 ? 2 : 1) void sdpa_bwd_kv_mfma(con
 
 typedef __attribute__((address_space(3))) void lds_void;
 constexpr int WAIT_VMEM = 0x0F70;  // s_waitcnt immediate: vmcnt(0), other counters free
-// vmcnt(4): all but the 4 newest vector memory operations done. Vector memory operations (loads,
-// LDS DMA copies and stores alike) retire in the order they were issued on this architecture, so
-// this waits for everything issued before the 4 newest.
-constexpr int WAIT_VMEM_BUT_4 = 0x0F74;
+// s_waitcnt immediate for vmcnt(n), n < 64, the other counters free: all but the n newest vector
+// memory operations done. Vector memory operations (loads, LDS DMA copies and stores alike)
+// retire in the order they were issued on this architecture, so this waits for everything issued
+// before the n newest.
+__host__ __device__ constexpr int wait_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 // cache policy of a buffer access (gfx940 family): nt, streamed past the caches. The dS hand-off
 // is written once and read once, gigabytes a step; left cached, it evicts the re-read tiles.
 constexpr int AUX_NT = 2;
@@ -823,6 +825,34 @@ struct DmaTile128 {
 #pragma unroll
     for (int p = 0; p < PASSES; p++)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)((char*)tile + (p * WAVES + wave) * 1024), 16, voff[p], 0, 0, 0);
+  }
+};
+
+// The same copy shared by the 8 waves of a two-waves-per-SIMD workgroup, this wave's eighth. (A
+// separate struct: as a template over the wave count, hipcc's host pass dropped the launch stubs
+// of the kernels that construct it.)
+struct DmaTile128x8 {
+  static constexpr int NW = 8, RB = 256, PASSES = TILE * RB / 1024 / NW;
+  const char* base;
+  int64_t bytes;
+  int voff[PASSES];
+  __device__ __forceinline__ DmaTile128x8(const u16* m, int rows, int wave, int lane) {
+    base = (const char*)m;
+    bytes = (int64_t)rows * RB;
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+      const int r = (p * NW + wave) * (1024 / RB) + lane / (RB / 16), pos = lane % (RB / 16);
+      voff[p] = r * RB + ((pos ^ swz128(r)) * 16);
+    }
+  }
+  // rows past the end read as zeros (the resource ends at the matrix)
+  __device__ __forceinline__ void copy(u16* tile, int row0, int wave) const {
+    const int64_t off = (int64_t)row0 * RB, left = bytes - off;
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(base + off), (short)0, (int)(left > 0 ? left : 0), 0x00020000);
+#pragma unroll
+    for (int p = 0; p < PASSES; p++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)((char*)tile + (p * NW + wave) * 1024), 16, voff[p], 0, 0, 0);
   }
 };
 
@@ -1057,63 +1087,86 @@ struct DsLayout {
   __host__ __device__ int64_t units_per_head() const { return first_unit(nkb); }
 };
 
-// ---- dK/dV pass at D = 128 without a key mask: software-pipelined ------------------------------
-// The same products as sdpa_bwd_kv_dma, reordered so the matrix cores never wait on the softmax.
-// A 32-query half goes through two phases of 16 MFMAs each:
-//   X: S and dP of the *next* half (S with Q rows, dP with dO rows, alternating: two independent
-//      accumulation chains), while the VALU turns the current half's S and dP into P and dS;
-//   Y: dV^T += dO^T P and dK^T += Q^T dS of the current half (transposing reads).
-// Every slot (one MFMA plus its share of LDS reads and VALU) is fenced with sched_barrier and its
-// VALU results pinned by an empty asm, so the interleave survives both the IR optimizer (which
-// would otherwise sink the softmax down to its first use) and the scheduler. The X phase of a
-// tile's second half reads the *next* tile's rows, so tiles are triple-buffered: tile t is read,
-// t + 1 is resident, t + 2 is in flight; the loop is unrolled by three so every buffer is a
-// separate __shared__ array at a fixed address (the copy into the idle buffer provably never
-// aliases a read). Causal tiles after the first two are whole, and rows past t_q (a ragged last
-// tile, and up to two padding tiles that round the loop to whole triples) arrive as zeros with
-// zero statistics: P = 1 there but dS = 0 and dO = 0, so they add nothing. Without a key mask no
-// tile but the two diagonal ones is masked; masked calls keep sdpa_bwd_kv_dma.
-// Measured on the MI355X at 128 heads x 4096 rows, causal (the C4 step): 1.144 ms against 1.273
-// for sdpa_bwd_kv_dma, identical results; a probe of this pass with its VALU and LDS reads
-// removed runs at 1350 TFLOP/s (the MFMAs alone at 2100), and one wave per SIMD hides only a few
-// VALU instructions per MFMA of its own, which is what bounds both kernels.
+// ---- dK/dV pass at D = 128 without a key mask: two waves per SIMD -------------------------------
+// A workgroup owns 128 keys and is 8 waves: wave w takes keys 32 (w % 4) .. + 31 and queries
+// 32 (w / 4) .. + 31 of every 64-query tile, and computes all four products of that 32 x 32
+// piece: S = Q K^T and dP = dO V^T (two independent chains over the head dim), P and
+// dS = P (dP - delta) scale, then dV^T += dO^T P and dK^T += Q^T dS (transposing reads). The
+// block's K and V rows sit in LDS (64 KiB, read as the B operands of S and dP) rather than in
+// registers, so a wave fits in 256 registers and two share a SIMD: one's softmax and LDS reads run
+// under the other's MFMAs. Each wave reads its operands one 16-deep step ahead. Q and dO tiles
+// are double-buffered by DMA, one barrier per tile; the two waves of a key group add their
+// partial dK and dV at the end (through LDS, the second query half's onto the first's, in that
+// order, so two runs give the same bits). Causal tiles after the first two (which hold the
+// block's diagonal) need no mask; rows past t_q arrive as zeros with zero statistics, so P = 1
+// there but dS = dO = 0 and they add nothing. Without a key mask no tile but the two diagonal
+// ones is masked; masked calls keep sdpa_bwd_kv_dma.
+// Measured on the MI355X at 128 heads x 4096 rows, causal, with the dS hand-off (the C4 step),
+// alternating builds on one box: 1.189-1.243 ms against 1.257-1.320 for the single-wave pass it
+// replaced (K/V in registers, 236 VGPRs + 220 AGPRs, one wave per SIMD, the softmax
+// software-pipelined against the next half's products); the same 8-wave pass reading its operands
+// in the step rather than one step ahead ran 1.277 against 1.270.
+//
+// With STORE_DS the pass also hands dS to the dQ pass (sdpa_dq_ds): each 16-query chunk's dS,
+// packed as the B operand of its dK product, goes out as it is, one 16-byte store per lane, into
+// the layout DsLayout describes (the key group is the block's "wave", the query half its "half").
+// The stores go through a buffer resource per tile whose size is zero for the tile past the
+// end, so that one is dropped without a branch.
+constexpr int KV_WAVES = 8;
 
-// With STORE_DS the pass also hands dS to the dQ pass (sdpa_dq_ds): each half's dS, already packed as
-// the B operand of its dK product, goes out as it is, one 16-byte store per lane and 16-query
-// chunk, into the layout DsLayout describes. The stores go through a buffer resource per tile
-// whose size is zero for the padding tiles past the end, so those are dropped without a branch.
 template <typename T, bool CAUSAL, bool STORE_DS>
-__global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_piped(const u16* __restrict__ q, const u16* __restrict__ k,
-                                                                const u16* __restrict__ v, const u16* __restrict__ dout,
-                                                                const float* __restrict__ lse,
-                                                                const float* __restrict__ delta, u16* __restrict__ dk,
-                                                                u16* __restrict__ dv, u16* __restrict__ dsout, int64_t batch,
-                                                                int t_q, int t_k, float scale) {
+__global__ __launch_bounds__(64 * KV_WAVES, 1) void sdpa_bwd_kv_dual(
+    const u16* __restrict__ q, const u16* __restrict__ k, const u16* __restrict__ v, const u16* __restrict__ dout,
+    const float* __restrict__ lse, const float* __restrict__ delta, u16* __restrict__ dk, u16* __restrict__ dv,
+    u16* __restrict__ dsout, int64_t batch, int t_q, int t_k, float scale) {
   constexpr int D = 128, ROWS = 128;
+  // The streamed tiles come first, in the low 64 KiB, where every read's LDS address is a lane
+  // offset plus the 16-bit immediate; K and V (the block's rows as two swizzled 64-row tiles
+  // each) follow, read at a lane offset that includes their base, V 32 KiB after K.
   __shared__ __attribute__((aligned(1024))) u16 Q0[TILE * D];
   __shared__ __attribute__((aligned(1024))) u16 Q1[TILE * D];
-  __shared__ __attribute__((aligned(1024))) u16 Q2[TILE * D];
   __shared__ __attribute__((aligned(1024))) u16 O0[TILE * D];
   __shared__ __attribute__((aligned(1024))) u16 O1[TILE * D];
-  __shared__ __attribute__((aligned(1024))) u16 O2[TILE * D];
-  __shared__ __attribute__((aligned(16))) float L0[TILE], L1[TILE], L2[TILE], D0[TILE], D1[TILE], D2[TILE];
+  __shared__ __attribute__((aligned(1024))) u16 Ks[ROWS * D];
+  __shared__ __attribute__((aligned(1024))) u16 Vs[ROWS * D];
+  __shared__ __attribute__((aligned(16))) float L0[TILE], L1[TILE], D0[TILE], D1[TILE];
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), h = lane >> 5, n = lane & 31;
+  const int kg = wave & 3, hq = wave >> 2;  // key group, query half
   int64_t b, kb;  // causal: the first keys are seen by the most queries
   head_and_block(batch, (t_k + ROWS - 1) / ROWS, b, kb);
-  const int k0 = (int)kb * ROWS, wk0 = k0 + wave * 32, key = wk0 + n;
-  const Rows krows(k + b * (int64_t)t_k * D, t_k, D), vrows(v + b * (int64_t)t_k * D, t_k, D);
-  const DmaTile128 qd(q + b * (int64_t)t_q * D, t_q, wave, lane), od(dout + b * (int64_t)t_q * D, t_q, wave, lane);
-  const SwzReads128 ad(lane);
+  const int k0 = (int)kb * ROWS, wk0 = k0 + kg * 32, key = wk0 + n;
+  const DmaTile128x8 kd(k + b * (int64_t)t_k * D, t_k, wave, lane), vd(v + b * (int64_t)t_k * D, t_k, wave, lane);
+  const DmaTile128x8 qd(q + b * (int64_t)t_q * D, t_q, wave, lane), od(dout + b * (int64_t)t_q * D, t_q, wave, lane);
   const float c2 = scale * LOG2E;
-
-  u16x8 kf[8], vf[8];
-  f32x16 gk[4], gv[4];
+  // per-lane byte offsets of every LDS read, the wave's rows folded in, so each read is one of
+  // these plus a compile-time offset (the arrays' own): rk by 16-deep step ds into Ks / Vs (this
+  // wave's 32 keys), rq by ds into a Q / dO tile (its 32 queries), rt by (dims 32 dt, half jj)
+  // for the transposing reads of its queries' first 16-query chunk (the second is 4 KiB on)
+  int rk[8], rq[8], rt[4][2];
+  {
+    const SwzReads128 ad(lane);
 #pragma unroll
-  for (int ds = 0; ds < 8; ds++) {
-    kf[ds] = krows.load8(key * D + ds * 16 + 8 * h);
-    vf[ds] = vrows.load8(key * D + ds * 16 + 8 * h);
+    for (int ds = 0; ds < 8; ds++) {
+      rk[ds] = ad.row[ds] + kg * 32 * 256;  // rows 32 kg + n of the two 64-row tiles, 16 KiB apart
+      rq[ds] = ad.row[ds] + hq * 32 * 256;
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) rt[dt][jj] = ad.tr[dt][jj] + hq * 32 * 256;
   }
+  auto rows_at = [](const u16* base, int off) __attribute__((always_inline)) {
+    return *(const u16x8*)((const char*)base + off);
+  };
+  auto transposed_at = [&](const u16* tile, int c, int dt) __attribute__((always_inline)) {
+    const char* p = (const char*)tile + c * 16 * 256;
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + rt[dt][0]));
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + rt[dt][1]));
+    return __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+
+  f32x16 gk[4], gv[4];
 #pragma unroll
   for (int dt = 0; dt < 4; dt++) {
     gk[dt] = zero16();
@@ -1121,15 +1174,7 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_piped(const u16* __res
   }
   const int qstart = CAUSAL ? k0 : 0;  // a causal key is seen by queries at or after it
   const int ntiles = qstart < t_q ? (t_q - qstart + TILE - 1) / TILE : 0;
-  if (ntiles == 0) {
-    store_transposed<T, D>(dk + b * (int64_t)t_k * D, gk, key, t_k, 1.f);
-    store_transposed<T, D>(dv + b * (int64_t)t_k * D, gv, key, t_k, 1.f);
-    return;
-  }
 
-  // a tile's statistics, loaded by every wave (the same values, so no branch splits the loop
-  // body) with the tile's copy and stored into LDS once the copy is waited for; entries past t_q
-  // read as zeros through the buffer resources
   const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc((void*)(lse + b * (int64_t)t_q), (short)0, t_q * 4, 0x00020000);
   const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc((void*)(delta + b * (int64_t)t_q), (short)0, t_q * 4, 0x00020000);
   float next_l = 0.f, next_d = 0.f;
@@ -1141,71 +1186,58 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_piped(const u16* __res
     L[lane] = next_l * LOG2E;
     Dl[lane] = next_d * scale;
   };
-  // the dS hand-off: this key block's units start at dsk, one per tile; lane and wave fix the
-  // 16 bytes a store writes inside a half's pair of blocks
   const DsLayout lay = DsLayout::of(t_q, t_k, CAUSAL);
   char* const dsk = STORE_DS ? (char*)dsout + ((int64_t)b * lay.units_per_head() + lay.first_unit((int)kb)) * DS_UNIT : nullptr;
-  const int ds_voff = wave * 4096 + lane * 16;
-  auto ds_tile = [&](int t) __attribute__((always_inline)) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)(STORE_DS ? dsk + (int64_t)t * DS_UNIT : nullptr), (short)0,
-                                             STORE_DS && t < ntiles ? DS_UNIT : 0, 0x00020000);
-  };
+  const int ds_voff = kg * 4096 + hq * 2048 + lane * 16;
 
-  f32x16 sA, dA, sB, dB;  // S and dP of a tile's first (A) and second (B) half
-  u16x8 xr[4], yr[4];     // operand rings of the X and Y phases, 3 reads ahead
-  f32x4 l4[4], d4[4];     // the statistics of the half an X phase's VALU works on
-  u16x8 pb[2], gb[2];     // that half's P and dS, packed for the Y phase
-
-  // X-phase MFMA i: S (even, Q rows) or dP (odd, dO rows) for ds = i / 2
-  auto xrow = [&](const u16* Qb, const u16* Ob, int sub, int i) __attribute__((always_inline)) {
-    return (i & 1) ? ad.rows(Ob, sub, i >> 1) : ad.rows(Qb, sub, i >> 1);
-  };
-  // Y-phase MFMA i: dV (even, dO^T) or dK (odd, Q^T) for 16-query chunk c = i / 8, dims 32 dt
-  auto ytr = [&](const u16* Qb, const u16* Ob, int sub, int i) __attribute__((always_inline)) {
-    const int c = i >> 3, dt = (i >> 1) & 3;
-    return (i & 1) ? ad.transposed(Qb, sub * 32 + 16 * c, dt) : ad.transposed(Ob, sub * 32 + 16 * c, dt);
-  };
-  auto stats_read = [&](const float* Lb, const float* Db, int sub, int g) __attribute__((always_inline)) {
-    l4[g] = *(const f32x4*)(Lb + sub * 32 + 8 * g + 4 * h);
-    d4[g] = *(const f32x4*)(Db + sub * 32 + 8 * g + 4 * h);
-  };
-  // X phase: MFMAs into (s, dp) for half xsub of (Qx, Ox) (their first 3 rows already read);
-  // VALU: P and dS of (ps, pd), half vsub of the tile at query r0, into pb, gb; its last slots
-  // read the first 3 operands of the Y phase that follows (half ysub of Qy, Oy)
-  auto xphase = [&](auto edge, f32x16& s, f32x16& dp, const u16* Qx, const u16* Ox, int xsub, f32x16& ps, f32x16& pd,
-                    int r0, int vsub, const u16* Qy, const u16* Oy, int ysub) __attribute__((always_inline)) {
+  // one tile of this wave's 32 queries (half hq of the tile at r0) against its 32 keys
+  auto tile = [&](auto edge, int t, const u16* Qc, const u16* Oc, const float* Lc, const float* Dc) __attribute__((always_inline)) {
     constexpr bool EDGE = decltype(edge)::value;
-    s = zero16();
-    dp = zero16();
+    const int r0 = qstart + t * TILE;
+    // the K and V rows are the same every tile: kept from hoisting their reads out of the tile
+    // loop, which would hold them in 64 registers (what this pass moves to LDS)
+    asm volatile("" ::: "memory");
+    f32x16 s = zero16(), dp = zero16();
+    // S = Q K^T and dP = dO V^T, 16-deep steps over the head dim, two chains, each step's four
+    // operands read one step ahead (deeper, they would not fit two waves' registers)
+    u16x8 xa[2][4];
+    auto xread = [&](int ds, u16x8* o) __attribute__((always_inline)) {
+      o[0] = rows_at(Qc, rq[ds]); o[1] = rows_at(Ks, rk[ds]); o[2] = rows_at(Oc, rq[ds]); o[3] = rows_at(Vs, rk[ds]);
+    };
+    xread(0, xa[0]);
+#pragma unroll
+    for (int ds = 0; ds < 8; ds++) {
+      if (ds + 1 < 8) xread(ds + 1, xa[(ds + 1) & 1]);
+      s = T::mfma32(xa[ds & 1][0], xa[ds & 1][1], s);
+      dp = T::mfma32(xa[ds & 1][2], xa[ds & 1][3], dp);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     unsigned pk[8], gk2[8];
     float pv = 0.f, gv2 = 0.f;
+    f32x4 l4, d4;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      if (i + 3 < 16) xr[(i + 3) % 4] = xrow(Qx, Ox, xsub, i + 3);
-      if (i >= 13) yr[i - 13] = ytr(Qy, Oy, ysub, i - 13);
-      if (i & 1)
-        dp = T::mfma32(xr[i % 4], vf[i >> 1], dp);
-      else
-        s = T::mfma32(xr[i % 4], kf[i >> 1], s);
-      float p = fast_exp2(fmaf(ps[i], c2, -l4[i >> 2][i & 3]));
+      if ((i & 3) == 0) {
+        l4 = *(const f32x4*)(Lc + hq * 32 + 8 * (i >> 2) + 4 * h);
+        d4 = *(const f32x4*)(Dc + hq * 32 + 8 * (i >> 2) + 4 * h);
+      }
+      float p = fast_exp2(fmaf(s[i], c2, -l4[i & 3]));
       if (EDGE) {
-        const int qq = r0 + vsub * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        const int qq = r0 + hq * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
         bool hide = (qq >= t_q) | (key >= t_k);
         if (CAUSAL) hide |= qq < key;
         p = hide ? 0.f : p;
       }
-      const float g = p * fmaf(pd[i], scale, -d4[i >> 2][i & 3]);
+      const float g = p * fmaf(dp[i], scale, -d4[i & 3]);
       if (i & 1) {
         pk[i >> 1] = T::pack2(pv, p);
         gk2[i >> 1] = T::pack2(gv2, g);
-        asm volatile("" : "+v"(pk[i >> 1]), "+v"(gk2[i >> 1]));
       } else {
         pv = p;
         gv2 = g;
-        asm volatile("" : "+v"(pv), "+v"(gv2));
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
+    u16x8 pb[2], gb[2];
 #pragma unroll
     for (int c = 0; c < 2; c++) {
       const u32x4 wp = {pk[4 * c], pk[4 * c + 1], pk[4 * c + 2], pk[4 * c + 3]};
@@ -1213,101 +1245,104 @@ __global__ __launch_bounds__(THREADS, 1) void sdpa_bwd_kv_piped(const u16* __res
       pb[c] = __builtin_bit_cast(u16x8, wp);
       gb[c] = __builtin_bit_cast(u16x8, wg);
     }
-  };
-  // Y phase: dV/dK MFMAs of half ysub of (Qy, Oy); its first slots read the statistics of the next
-  // X phase's VALU half (Ls, Ds, half ssub), its last slots that X phase's first rows (Qx, Ox, xsub);
-  // with STORE_DS its first two slots also store the half's dS (gb) through `dsr`
-  auto yphase = [&](const u16* Qy, const u16* Oy, int ysub, const float* Ls, const float* Ds, int ssub, const u16* Qx,
-                    const u16* Ox, int xsub, __amdgpu_buffer_rsrc_t dsr) __attribute__((always_inline)) {
+    if (STORE_DS) {
+      const __amdgpu_buffer_rsrc_t dsr = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(dsk + (int64_t)t * DS_UNIT), (short)0, t < ntiles ? DS_UNIT : 0, 0x00020000);
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      if (i + 3 < 16) yr[(i + 3) % 4] = ytr(Qy, Oy, ysub, i + 3);
-      if (i < 4) stats_read(Ls, Ds, ssub, i);
-      if (i >= 13) xr[i - 13] = xrow(Qx, Ox, xsub, i - 13);
-      if (STORE_DS && i < 2)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, gb[i]), dsr, ds_voff + ysub * 2048 + i * 1024, 0, AUX_NT);
-      const int c = i >> 3, dt = (i >> 1) & 3;
-      if (i & 1)
-        gk[dt] = T::mfma32(yr[i % 4], gb[c], gk[dt]);
-      else
-        gv[dt] = T::mfma32(yr[i % 4], pb[c], gv[dt]);
+      for (int c = 0; c < 2; c++)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, gb[c]), dsr, ds_voff + c * 1024, 0, AUX_NT);
+    }
+    // dV^T += dO^T P and dK^T += Q^T dS over the half's two 16-query chunks
+    u16x8 ya[2][2];
+    auto yread = [&](int j, u16x8* o) __attribute__((always_inline)) {
+      o[0] = transposed_at(Oc, j >> 2, j & 3); o[1] = transposed_at(Qc, j >> 2, j & 3);
+    };
+    yread(0, ya[0]);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      if (j + 1 < 8) yread(j + 1, ya[(j + 1) & 1]);
+      const int c = j >> 2, dt = j & 3;
+      gv[dt] = T::mfma32(ya[j & 1][0], pb[c], gv[dt]);
+      gk[dt] = T::mfma32(ya[j & 1][1], gb[c], gk[dt]);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-
-  // prologue: tile 0 resident with its statistics, tile 1 in flight, S and dP of tile 0's first half
-  qd.copy(Q0, qstart, wave);
-  od.copy(O0, qstart, wave);
-  stats_load(qstart);
-  __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
-  stats_store(L0, D0);
-  qd.copy(Q1, qstart + TILE, wave);
-  od.copy(O1, qstart + TILE, wave);
-  stats_load(qstart + TILE);
-  __syncthreads();
-  sA = zero16();
-  dA = zero16();
-#pragma unroll
-  for (int i = 0; i < 3; i++) xr[i] = xrow(Q0, O0, 0, i);
-#pragma unroll
-  for (int i = 0; i < 16; i++) {
-    if (i + 3 < 16) xr[(i + 3) % 4] = xrow(Q0, O0, 0, i + 3);
-    if (i < 4) stats_read(L0, D0, 0, i);
-    if (i & 1)
-      dA = T::mfma32(xr[i % 4], vf[i >> 1], dA);
-    else
-      sA = T::mfma32(xr[i % 4], kf[i >> 1], sA);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-#pragma unroll
-  for (int i = 0; i < 3; i++) xr[i] = xrow(Q0, O0, 1, i);
-
-  // tile t in (Qc, Oc, Lc, Dc); tile t + 1 arriving in (Qn, On), its statistics in registers;
-  // (Qf, Of) free for tile t + 2 once every wave passes this step's barrier
-  // The wait in the middle of a step is for the copies of tile t + 1 (and its statistics),
-  // issued in the step before. With STORE_DS that step also issued the 4 stores of tile t - 1's
-  // dS after those copies, and they need not be waited for: every step but the first waits for
-  // all but the 4 newest operations (waiting for all made the stores' write acknowledgements part
-  // of every tile's critical path).
-  auto step = [&](auto edge, auto first, int t, const u16* Qc, const u16* Oc, const float* Lc, const float* Dc,
-                  const u16* Qn, const u16* On, float* Ln, float* Dn, u16* Qf, u16* Of) __attribute__((always_inline)) {
-    const int r0 = qstart + t * TILE;
-    const __amdgpu_buffer_rsrc_t dsr = ds_tile(t);
-    xphase(edge, sB, dB, Qc, Oc, 1, sA, dA, r0, 0, Qc, Oc, 0);  // S/dP of half 1, P/dS of half 0
-    __builtin_amdgcn_s_waitcnt(STORE_DS && !decltype(first)::value ? WAIT_VMEM_BUT_4 : WAIT_VMEM);
+  // tile t from (Qc, Oc, Lc, Dc) while tile t + 1 is copied into (Qn, On) and its statistics
+  // loaded; then the wait for those copies (all but the newest two operations, this tile's dS
+  // stores, which need not be waited for), the statistics into (Ln, Dn), and the barrier
+  auto step = [&](auto edge, int t, const u16* Qc, const u16* Oc, const float* Lc, const float* Dc, u16* Qn, u16* On,
+                  float* Ln, float* Dn) __attribute__((always_inline)) {
+    const int r1 = qstart + (t + 1) * TILE;
+    qd.copy(Qn, r1, wave);
+    od.copy(On, r1, wave);
+    stats_load(r1);
+    __builtin_amdgcn_sched_barrier(0);  // the copies and loads issue before this tile's dS stores
+    tile(edge, t, Qc, Oc, Lc, Dc);
+    __builtin_amdgcn_s_waitcnt(STORE_DS ? wait_vm(2) : WAIT_VMEM);
     stats_store(Ln, Dn);
     __syncthreads();
-    qd.copy(Qf, r0 + 2 * TILE, wave);
-    od.copy(Of, r0 + 2 * TILE, wave);
-    stats_load(r0 + 2 * TILE);
-    __builtin_amdgcn_sched_barrier(0);  // the copies and loads issue before the stores below
-    yphase(Qc, Oc, 0, Lc, Dc, 1, Qn, On, 0, dsr);                // dV/dK of half 0
-    xphase(edge, sA, dA, Qn, On, 0, sB, dB, r0, 1, Qc, Oc, 1);  // S/dP of the next tile's half 0, P/dS of half 1
-    yphase(Qc, Oc, 1, Ln, Dn, 0, Qn, On, 1, dsr);                // dV/dK of half 1
   };
-  constexpr std::true_type masked{}, first{};
-  constexpr std::false_type whole{}, later{};
-  if (CAUSAL) {
-    step(masked, first, 0, Q0, O0, L0, D0, Q1, O1, L1, D1, Q2, O2);
-    if (ntiles > 1) step(masked, later, 1, Q1, O1, L1, D1, Q2, O2, L2, D2, Q0, O0);
-    for (int t = 2; t < ntiles; t += 3) {
-      step(whole, later, t, Q2, O2, L2, D2, Q0, O0, L0, D0, Q1, O1);
-      step(whole, later, t + 1, Q0, O0, L0, D0, Q1, O1, L1, D1, Q2, O2);
-      step(whole, later, t + 2, Q1, O1, L1, D1, Q2, O2, L2, D2, Q0, O0);
+  if (ntiles > 0) {
+    kd.copy(Ks, k0, wave);
+    kd.copy(Ks + TILE * D, k0 + TILE, wave);
+    vd.copy(Vs, k0, wave);
+    vd.copy(Vs + TILE * D, k0 + TILE, wave);
+    qd.copy(Q0, qstart, wave);
+    od.copy(O0, qstart, wave);
+    stats_load(qstart);
+    __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
+    stats_store(L0, D0);
+    __syncthreads();
+    constexpr std::true_type masked{};
+    constexpr std::false_type whole{};
+    // the first two tiles of a causal block hold its diagonal
+    int t = 0;
+    if (CAUSAL) {
+      step(masked, 0, Q0, O0, L0, D0, Q1, O1, L1, D1);
+      if (ntiles > 1) step(masked, 1, Q1, O1, L1, D1, Q0, O0, L0, D0);
+      t = 2;
     }
-  } else {
-    step(whole, first, 0, Q0, O0, L0, D0, Q1, O1, L1, D1, Q2, O2);
-    for (int t = 1; t < ntiles; t += 3) {
-      step(whole, later, t, Q1, O1, L1, D1, Q2, O2, L2, D2, Q0, O0);
-      step(whole, later, t + 1, Q2, O2, L2, D2, Q0, O0, L0, D0, Q1, O1);
-      step(whole, later, t + 2, Q0, O0, L0, D0, Q1, O1, L1, D1, Q2, O2);
+    for (; t + 1 < ntiles; t += 2) {
+      step(whole, t, Q0, O0, L0, D0, Q1, O1, L1, D1);
+      step(whole, t + 1, Q1, O1, L1, D1, Q0, O0, L0, D0);
     }
+    if (t < ntiles) step(whole, t, Q0, O0, L0, D0, Q1, O1, L1, D1);
   }
-  __builtin_amdgcn_s_waitcnt(WAIT_VMEM);  // the copies issued for tiles past the end
-  __syncthreads();                        // every wave is done with the tile buffers
-  u16* stage = wave == 0 ? Q0 : wave == 1 ? Q1 : wave == 2 ? O0 : O1;
-  store_staged<T, 128>(dk + b * (int64_t)t_k * D, gk, wk0, t_k, 1.f, stage);
-  store_staged<T, 128>(dv + b * (int64_t)t_k * D, gv, wk0, t_k, 1.f, stage);
+  __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
+  __syncthreads();  // every wave is done with every buffer
+  // the second query half's partials to LDS, in its accumulators' own lane order, 16 KiB per
+  // matrix: key group 0 in Ks, 1 in Vs, 2 in Q0 / Q1, 3 in O0 / O1
+  char* const part_k = kg == 0 ? (char*)Ks : kg == 1 ? (char*)Vs : kg == 2 ? (char*)Q0 : (char*)O0;
+  char* const part_v = kg == 0 ? (char*)Ks + 16384 : kg == 1 ? (char*)Vs + 16384 : kg == 2 ? (char*)Q1 : (char*)O1;
+  if (hq == 1) {
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        *(f32x4*)(part_k + ((dt * 4 + e) * 64 + lane) * 16) = f32x4{gk[dt][4 * e], gk[dt][4 * e + 1], gk[dt][4 * e + 2], gk[dt][4 * e + 3]};
+        *(f32x4*)(part_v + ((dt * 4 + e) * 64 + lane) * 16) = f32x4{gv[dt][4 * e], gv[dt][4 * e + 1], gv[dt][4 * e + 2], gv[dt][4 * e + 3]};
+      }
+  }
+  __syncthreads();
+  if (hq == 0) {
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const f32x4 pk4 = *(const f32x4*)(part_k + ((dt * 4 + e) * 64 + lane) * 16);
+        const f32x4 pv4 = *(const f32x4*)(part_v + ((dt * 4 + e) * 64 + lane) * 16);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          gk[dt][4 * e + j] = gk[dt][4 * e + j] + pk4[j];
+          gv[dt][4 * e + j] = gv[dt][4 * e + j] + pv4[j];
+        }
+      }
+    // staged through this key group's dK partial area (8704 of its 16384 bytes), which only this
+    // wave reads from now on (LDS runs a wave's operations in order)
+    u16* stage = (u16*)part_k;
+    store_staged<T, 128>(dk + b * (int64_t)t_k * D, gk, wk0, t_k, 1.f, stage);
+    store_staged<T, 128>(dv + b * (int64_t)t_k * D, gv, wk0, t_k, 1.f, stage);
+  }
 }
 
 // ---- dQ pass from the handed-over dS (D = 128) --------------------------------------------------
@@ -1419,7 +1454,7 @@ template <typename T, bool CAUSAL, bool STORE_DS>
 int launch_kv128(const SdpaArgs& a, u16* dk, u16* dv, u16* ds) {
   const int64_t blocks = a.batch * ((a.t_k + 127) / 128);
   if (blocks > 0x7fffffff) return fail(LIMN_HIP_EUNSUPPORTED, "sdpa: %lld workgroups exceed one launch", (long long)blocks);
-  hipLaunchKernelGGL((sdpa_bwd_kv_piped<T, CAUSAL, STORE_DS>), dim3((unsigned)blocks), dim3(THREADS), 0, a.stream,
+  hipLaunchKernelGGL((sdpa_bwd_kv_dual<T, CAUSAL, STORE_DS>), dim3((unsigned)blocks), dim3(64 * KV_WAVES), 0, a.stream,
                      (const u16*)a.q, (const u16*)a.k, (const u16*)a.v, (const u16*)a.dout, (const float*)a.lse,
                      (const float*)a.delta, dk, dv, ds, a.batch, (int)a.t_q, (int)a.t_k, (float)a.scale);
   return check_hip(hipGetLastError(), "launching the dK/dV pass");
