@@ -1484,21 +1484,20 @@ int launch_bwd_ds(const SdpaArgs& a, void* ws, int passes) {
 // causal block's two diagonal tiles, a last tile past t_k, every tile under a key mask) run
 // their own instance of the tile body.
 
-// one 64-key tile against the wave's 32 resident queries: S^T for both 32-key halves, one online
-// softmax step for the 64 keys (the reference point moves only when the tile's max passes it by
-// `lift`), then the V^T P^T products. One step per 64 keys rather than per 32 halves the serial
-// max / exchange / test chain per key; measured 0.566 ms against 0.587 for the forward at 128
-// heads x 4096 rows, causal (the results differ in rounding: P's reference point moves less often)
-template <typename T, bool CAUSAL, bool MASK, bool EDGE>
-__device__ __forceinline__ void fwd_tile128(const u16* Kb, const u16* Vb, const SwzReads128& ad, int k0, int row, int t_k,
-                                            float c2, float lift, uint64_t live, const u16x8 (&qf)[8], f32x16 (&acc)[4],
-                                            float& m, float& l) {
+// Each wave keeps 32 queries resident and walks 64-key tiles: S^T for both 32-key halves, one
+// online softmax step for the 64 keys (the reference point moves only when the tile's max passes
+// it by `lift`), then the V^T P^T products. One step per 64 keys rather than per 32 halves the
+// serial max / exchange / test chain per key; measured 0.566 ms against 0.587 for the forward at
+// 128 heads x 4096 rows, causal (the results differ in rounding: P's reference point moves less
+// often).
+
+// The online-softmax update for one 64-key tile of S^T (both 32-key halves, masked when EDGE):
+// the tile's max, and when it passes the reference point by more than `lift`, the new reference
+// with l and the accumulators rescaled to it
+template <bool CAUSAL, bool MASK, bool EDGE>
+__device__ __forceinline__ void fwd_max128(f32x16 (&s)[2], int k0, int row, int t_k, float c2, float lift, uint64_t live,
+                                           f32x16 (&acc)[4], float& m, float& l) {
   const int lane = threadIdx.x & 63, h = lane >> 5;
-  f32x16 s[2] = {zero16(), zero16()};
-#pragma unroll
-  for (int ds = 0; ds < 8; ds++)
-#pragma unroll
-    for (int sub = 0; sub < 2; sub++) s[sub] = T::mfma32(ad.rows(Kb, sub, ds), qf[ds], s[sub]);
   if (EDGE) {
 #pragma unroll
     for (int sub = 0; sub < 2; sub++) {
@@ -1521,6 +1520,34 @@ __device__ __forceinline__ void fwd_tile128(const u16* Kb, const u16* Vb, const 
     for (int dt = 0; dt < 4; dt++) acc[dt] *= alpha;
     m = mnew;
   }
+}
+
+// S^T of one 64-key tile against the wave's 32 resident queries, both 32-key halves
+template <typename T>
+__device__ __forceinline__ void fwd_scores128(const u16* Kb, const SwzReads128& ad, const u16x8 (&qf)[8], f32x16 (&s)[2]) {
+  s[0] = zero16();
+  s[1] = zero16();
+#pragma unroll
+  for (int ds = 0; ds < 8; ds++)
+#pragma unroll
+    for (int sub = 0; sub < 2; sub++) s[sub] = T::mfma32(ad.rows(Kb, sub, ds), qf[ds], s[sub]);
+}
+
+// One pipelined step of the forward: the probabilities of tile `it` (its S^T in `s`, the reference
+// point already moved for it) and the V^T P^T products from Vc, while the S^T products of tile
+// it + 1 (from Kn) run on the matrix cores; then tile it + 1's online-softmax update. The
+// exponentials of one tile and the scores of the next are independent, so the wave issues VALU
+// work while its own MFMAs execute instead of waiting on them. Same operations in the same order
+// per element as one tile at a time, so the same bits. Measured on the MI355X at 128 heads x 4096
+// rows, causal, alternating builds on one box: 0.544-0.550 ms against 0.560-0.566 for one tile at
+// a time; pinning the interleave (one LDS read and six VALU instructions per MFMA, by
+// sched_group_barrier) ran 0.552-0.558, the compiler's own order is kept.
+template <typename T, bool CAUSAL, bool MASK, bool EDGE_NEXT, bool HAS_NEXT>
+__device__ __forceinline__ void fwd_pipe128(const u16* Kn, const u16* Vc, const SwzReads128& ad, int kn0, int row, int t_k,
+                                            float c2, float lift, uint64_t live_next, const u16x8 (&qf)[8],
+                                            f32x16 (&acc)[4], f32x16 (&s)[2], float& m, float& l) {
+  f32x16 sn[2];
+  if (HAS_NEXT) fwd_scores128<T>(Kn, ad, qf, sn);
   const float base = m == neg_inf() ? 0.f : m * c2;
   float rs = 0.f;
 #pragma unroll
@@ -1538,8 +1565,13 @@ __device__ __forceinline__ void fwd_tile128(const u16* Kb, const u16* Vb, const 
     for (int c = 0; c < 2; c++) {
       const u16x8 pb = pack8<T>(s[sub], 8 * c);
 #pragma unroll
-      for (int dt = 0; dt < 4; dt++) acc[dt] = T::mfma32(ad.transposed(Vb, sub * 32 + 16 * c, dt), pb, acc[dt]);
+      for (int dt = 0; dt < 4; dt++) acc[dt] = T::mfma32(ad.transposed(Vc, sub * 32 + 16 * c, dt), pb, acc[dt]);
     }
+  if (HAS_NEXT) {
+    fwd_max128<CAUSAL, MASK, EDGE_NEXT>(sn, kn0, row, t_k, c2, lift, live_next, acc, m, l);
+    s[0] = sn[0];
+    s[1] = sn[1];
+  }
 }
 
 template <typename T, bool CAUSAL, bool MASK>
@@ -1566,7 +1598,7 @@ __global__ __launch_bounds__(THREADS, 2) void sdpa_fwd_dma(const u16* __restrict
   const float c2 = scale * LOG2E, lift = RESCALE_LOG2 / c2;  // scale > 0 (the C ABI routes others away)
 
   u16x8 qf[8];
-  f32x16 acc[4];
+  f32x16 acc[4], s[2];
   float m = neg_inf(), l = 0.f;
 #pragma unroll
   for (int ds = 0; ds < 8; ds++) qf[ds] = qrows.load8(row * D + ds * 16 + 8 * h);
@@ -1575,44 +1607,58 @@ __global__ __launch_bounds__(THREADS, 2) void sdpa_fwd_dma(const u16* __restrict
 
   const int kend = CAUSAL ? (q0 + ROWS < t_k ? q0 + ROWS : t_k) : t_k;
   const int ntiles = (kend + TILE - 1) / TILE;
-  // tile it from (Kc, Vc) while tile it + 1 is copied into the idle buffers (every wave left them
-  // at the last barrier), then the wait for the copy and the barrier
-  auto step = [&](auto edge, int it, const u16* Kc, const u16* Vc, u16* Kn, u16* Vn) __attribute__((always_inline)) {
-    const int k0 = it * TILE;
-    kd.copy(Kn, k0 + TILE, wave);
-    vd.copy(Vn, k0 + TILE, wave);
-    const uint64_t live = MASK ? live_keys<T>(mrow.load(k0 + lane)) : ~0ull;
-    fwd_tile128<T, CAUSAL, MASK, decltype(edge)::value>(Kc, Vc, ad, k0, row, t_k, c2, lift, live, qf, acc, m, l);
-    __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
-    __syncthreads();
-  };
-  // tiles [from, to) with one body: tile it is in buffer it % 2
-  auto run = [&](auto edge, int from, int to) __attribute__((always_inline)) {
-    int it = from;
-    if ((it & 1) && it < to) {
-      step(edge, it, K1, V1, K0, V0);
-      it++;
-    }
-    for (; it + 1 < to; it += 2) {
-      step(edge, it, K0, V0, K1, V1);
-      step(edge, it + 1, K1, V1, K0, V0);
-    }
-    if (it < to) step(edge, it, K0, V0, K1, V1);
-  };
-  if (ntiles > 0) {
-    kd.copy(K0, 0, wave);
-    vd.copy(V0, 0, wave);
-    __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
-    __syncthreads();
-  }
   // unmasked: every key of the tile exists and, under causality, precedes the block's first row
   int open = MASK ? 0 : t_k / TILE;
   if (CAUSAL && q0 / TILE < open) open = q0 / TILE;
   if (open > ntiles) open = ntiles;
-  run(std::false_type{}, 0, open);
-  run(std::true_type{}, open, ntiles);
+  auto live_of = [&](int k0) __attribute__((always_inline)) { return MASK ? live_keys<T>(mrow.load(k0 + lane)) : ~0ull; };
+  // Tile it's probabilities and V^T P^T from buffer it % 2, tile it + 1's scores from K buffer
+  // (it + 1) % 2, while K of tile it + 2 is copied into K buffer it % 2 and V of tile it + 1
+  // into V buffer (it + 1) % 2 (both last read before the previous barrier); then the wait for
+  // the copies and the barrier
+  auto step = [&](auto edge_next, int it, const u16* Kn, const u16* Vc, u16* Kf, u16* Vf) __attribute__((always_inline)) {
+    const int kn0 = (it + 1) * TILE;
+    kd.copy(Kf, kn0 + TILE, wave);
+    vd.copy(Vf, kn0, wave);
+    fwd_pipe128<T, CAUSAL, MASK, decltype(edge_next)::value, true>(Kn, Vc, ad, kn0, row, t_k, c2, lift, live_of(kn0), qf,
+                                                                    acc, s, m, l);
+    __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
+    __syncthreads();
+  };
+  // steps [from, to) whose next tiles share one masking body
+  auto run = [&](auto edge_next, int from, int to) __attribute__((always_inline)) {
+    int it = from;
+    if ((it & 1) && it < to) {
+      step(edge_next, it, K0, V1, K1, V0);
+      it++;
+    }
+    for (; it + 1 < to; it += 2) {
+      step(edge_next, it, K1, V0, K0, V1);
+      step(edge_next, it + 1, K0, V1, K1, V0);
+    }
+    if (it < to) step(edge_next, it, K1, V0, K0, V1);
+  };
+  if (ntiles > 0) {
+    kd.copy(K0, 0, wave);
+    vd.copy(V0, 0, wave);
+    kd.copy(K1, TILE, wave);
+    __builtin_amdgcn_s_waitcnt(WAIT_VMEM);
+    __syncthreads();
+    fwd_scores128<T>(K0, ad, qf, s);
+    if (open > 0)
+      fwd_max128<CAUSAL, MASK, false>(s, 0, row, t_k, c2, lift, live_of(0), acc, m, l);
+    else
+      fwd_max128<CAUSAL, MASK, true>(s, 0, row, t_k, c2, lift, live_of(0), acc, m, l);
+    __syncthreads();  // every wave's reads of K buffer 0 are done before tile 2 is copied there
+    // step it's next tile is it + 1: unmasked while it + 1 < open
+    const int last = ntiles - 1, split = open - 1 < 0 ? 0 : (open - 1 < last ? open - 1 : last);
+    run(std::false_type{}, 0, split);
+    run(std::true_type{}, split, last);
+    const u16* Vl = (last & 1) ? V1 : V0;
+    fwd_pipe128<T, CAUSAL, MASK, true, false>(K0, Vl, ad, 0, row, t_k, c2, lift, 0, qf, acc, s, m, l);
+    __syncthreads();  // the tile buffers become staging below
+  }
   const float total = pair_sum(l);
-  // the tile buffers are free: the last step waited for its copy and passed the barrier
   u16* stage = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? V0 : V1;
   store_staged<T, 128>(out + b * (int64_t)t_q * D, acc, q0 + wave * 32, t_q, 1.f / total, stage);
   if (h == 0 && row < t_q) lse[b * (int64_t)t_q + row] = m * scale + logf(total);
