@@ -152,10 +152,14 @@ MFMA_CASES = {
     "d64_ragged": ((2, 2, 200, 64), (2, 2, 200, 64), (2, 2, 200, 64)),
     "d128_two_blocks": ((1, 2, 256, 128), (1, 2, 256, 128), (1, 2, 256, 128)),
     "d128_ragged": ((2, 1, 333, 128), (2, 1, 333, 128), (2, 1, 333, 128)),
-    # the pipelined dK/dV pass: 10 and 13 query tiles per key block, loops of whole triples
-    # with padding tiles, a ragged last tile past the diagonal
+    # long heads: 10 and 13 query tiles per key block, tile loops unrolled by two with an odd
+    # count, a ragged last tile past the diagonal
     "d128_long": ((1, 2, 640, 128), (1, 2, 640, 128), (1, 2, 640, 128)),
     "d128_long_ragged": ((1, 1, 801, 128), (1, 1, 801, 128), (1, 1, 801, 128)),
+    # one and two 64-key tiles: the software-pipelined forward's prologue and last step with no
+    # steady-state step between them
+    "d128_one_tile": ((2, 1, 40, 128), (2, 1, 40, 128), (2, 1, 40, 128)),
+    "d128_two_tiles": ((1, 2, 100, 128), (1, 2, 100, 128), (1, 2, 100, 128)),
 }
 
 
