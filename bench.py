@@ -16,7 +16,10 @@ dK), sdpa_bwd_q 1U (dQ; its recomputed S and dP are executed, not algorithmic).
 
 Timing: W untimed warmup steps, then K steps between two hipEvents on the null stream with a
 device synchronize on both sides; per-kernel averages come from events recorded between the
-launches of every timed step.
+launches of every timed step. The boxes' clocks ramp up over tens of milliseconds of load: the
+default W (100 steps, 0.23 s of the headline) covers that, and the C1-C3 workloads, whose steps
+take well under a millisecond, also repeat their step untimed until SETTLE_S seconds have passed
+(`settle`) before the timed ones.
 
 roofline.traffic is the dominant kernel's HBM bytes per launch from profiles/hbm_traffic.json
 (rocprofv3 FETCH_SIZE/WRITE_SIZE passes reduced by `bench.py --summarize`); it is null when
@@ -103,7 +106,7 @@ def parse() -> argparse.Namespace:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--headline-only", action="store_true", help="the C4 line without the C1/C2/C3/C5 workloads "
                    "(for profiling the attention kernels alone)")
@@ -289,6 +292,23 @@ class Events:
         return float(out.value)
 
 
+SETTLE_S = 0.25  # seconds of untimed load before a sub-millisecond workload is timed
+
+
+def settle(dev, run_once, seconds: float = SETTLE_S) -> int:
+    """Untimed repetitions of one step, eight between synchronizations, until `seconds` of wall
+    time have passed; returns how many ran. Measured on the MI355X, C3's launch took 121, 112
+    and 105 µs in three back-to-back trials of 20 after a 10-step warmup: the clock was still
+    ramping."""
+    t0, n = time.perf_counter(), 0
+    while n == 0 or time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            run_once()
+        n += 8
+        dev.finish()
+    return n
+
+
 def c_device_run(build) -> float:
     """Seconds spent inside the compiled nests when the graph `build()` returns (a list of
     tensors) is realized on the CPU baseline: oracle/c_device.py, limn's single-threaded C backend
@@ -411,6 +431,8 @@ def bench_c2(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     for _ in range(warmup):
         timed_calls(dev, plan, sources, Events(dev.api, ncalls + 1), 0)
     dev.finish()
+    spare = Events(dev.api, ncalls + 1)
+    settled = settle(dev, lambda: timed_calls(dev, plan, sources, spare, 0))
     ev = Events(dev.api, steps * (ncalls + 1))
     for s_ in range(steps):
         timed_calls(dev, plan, sources, ev, s_ * (ncalls + 1))
@@ -477,6 +499,7 @@ def bench_c2(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
         "value": round(total / (chain_ms * 1e-3) / 1e9, 1),
         "unit": "GB/s",
         "ms_per_step": round(chain_ms, 4),
+        "settle_steps": settled,
         "dtype": "f32",
         "config": {"workload": f"C2 row softmax -> LayerNorm, x f32 (8192, 8192), {ncalls} scheduled kernels, {launched} launched", "bytes_per_step": total},
         "kernels": kernels,
@@ -523,6 +546,8 @@ def bench_c3(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     for _ in range(warmup):
         timed_calls(dev, plan, sources, Events(dev.api, ncalls + 1), 0)
     dev.finish()
+    spare = Events(dev.api, ncalls + 1)
+    settled = settle(dev, lambda: timed_calls(dev, plan, sources, spare, 0))
     ev = Events(dev.api, steps * (ncalls + 1))
     for s_ in range(steps):
         timed_calls(dev, plan, sources, ev, s_ * (ncalls + 1))
@@ -553,6 +578,7 @@ def bench_c3(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
         "value": round(flops / (step_ms * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s",
         "ms_per_step": round(step_ms, 4),
+        "settle_steps": settled,
         "dtype": "bf16",
         "config": {"workload": "C3 bf16 4096^3 contraction + relu + bf16 store", "flop_per_step": flops},
         "kernels_ms": [round(float(t), 4) for t in per],
@@ -621,6 +647,7 @@ def bench_c1(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     for _ in range(warmup):
         step()
     dev.finish()
+    settled = settle(dev, step)
     ev = Events(dev.api, 2)
     ev.record(0)
     for _ in range(steps):
@@ -640,6 +667,7 @@ def bench_c1(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     return {
         "metric": "sdpa fwd+bwd microseconds per step",
         "value": round(us, 2),
+        "settle_steps": settled,
         "unit": "us",
         "higher_is_better": False,
         "dtype": "f32",
