@@ -79,8 +79,10 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 // XCD then starts its longest blocks early, where heads one after another would leave the last
 // head's longest block to start near the end. Measured on the MI355X at 128 heads x 4096 rows,
 // causal: the forward took 0.604 ms with whole heads in order, 0.569 with pairs, 0.548 with
-// groups of 4 or 8, 0.554 with 16.
+// groups of 4 or 8, 0.554 with 16. The dQ pass from the handed-over dS takes groups of 8: 0.464
+// against 0.482 ms with 4, alternating builds on one box (0.459-0.464 with 16, 0.62 with 32).
 constexpr int HEAD_GROUP = 4;
+constexpr int DQ_HEAD_GROUP = 8;
 
 // Work units of the D = 64 passes per head: under causality a block and its mirror (the block
 // counted from the other end) make one unit, so every unit walks the same number of tiles. At
@@ -91,12 +93,13 @@ __host__ __device__ constexpr int64_t paired_units(int64_t blocks) {
   return CAUSAL ? (blocks + 1) / 2 : blocks;
 }
 
+template <int G = HEAD_GROUP>
 __device__ __forceinline__ void head_and_block(int64_t batch, int64_t nblocks, int64_t& b, int64_t& blk) {
   if (gridDim.x % 8 == 0) {
     const int64_t id = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
-    const int64_t group = id / (HEAD_GROUP * nblocks), r = id % (HEAD_GROUP * nblocks);
-    const int64_t heads = batch - HEAD_GROUP * group < HEAD_GROUP ? batch - HEAD_GROUP * group : HEAD_GROUP;
-    b = HEAD_GROUP * group + r % heads;
+    const int64_t group = id / (G * nblocks), r = id % (G * nblocks);
+    const int64_t heads = batch - G * group < G ? batch - G * group : G;
+    b = G * group + r % heads;
     blk = r / heads;
   } else {
     b = blockIdx.x % batch;
@@ -1386,7 +1389,7 @@ __global__ __launch_bounds__(THREADS, 2) void sdpa_dq_ds(const u16* __restrict__
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t nqb = (t_q + ROWS - 1) / ROWS;
   int64_t b, blk;
-  head_and_block(batch, nqb, b, blk);
+  head_and_block<DQ_HEAD_GROUP>(batch, nqb, b, blk);
   // heads in the reverse of the dK/dV pass's order: every XCD starts on a head whose dS that
   // pass wrote last, part of which the Infinity Cache still holds. Measured on the MI355X at 128
   // heads x 4096 rows, causal, alternating builds on one box: 0.4932 against 0.5011-0.5015 ms,
