@@ -19,7 +19,7 @@ device synchronize on both sides; per-kernel averages come from events recorded 
 launches of every timed step. The boxes' clocks ramp up over tens of milliseconds of load: the
 default W (100 steps, 0.23 s of the headline) covers that, and the C1-C3 workloads, whose steps
 take well under a millisecond, also repeat their step untimed until SETTLE_S seconds have passed
-(`settle`) before the timed ones.
+(`settle`) before the timed ones; C5 does the same in whole rotations of its batches.
 
 roofline.traffic is the dominant kernel's HBM bytes per launch from profiles/hbm_traffic.json
 (rocprofv3 FETCH_SIZE/WRITE_SIZE passes reduced by `bench.py --summarize`); it is null when
@@ -717,6 +717,14 @@ def bench_c5(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
             loss = fn(*batches[i % 4])
         first_loss = float(loss.item())
         dev.finish()
+        # then whole rotations until the clock has settled (SETTLE_S of load)
+        settled, t_settle = 0, time.perf_counter()
+        while time.perf_counter() - t_settle < SETTLE_S:
+            for i in range(done, done + len(batches)):
+                loss = fn(*batches[i % 4])
+            done += len(batches)
+            settled += len(batches)
+            dev.finish()
         issued = dev.issue_seconds
 
         def captures() -> int:
@@ -764,6 +772,7 @@ def bench_c5(dev, steps: int, warmup: int, with_cpu: bool = False) -> dict:
         "value": round(tok_s, 1),
         "unit": "tok/s",
         "ms_per_step": round(elapsed / steps * 1e3, 3),
+        "settle_steps": settled,
         "dtype": "bf16",
         "config": {"workload": "C5 byte-level GPT training step (captured), d512 L8 H8 ctx512 batch32, AdamW; "
                                "matmul in limn spelling (both operands broadcast to (batch, m, n, k), summed over k)",
