@@ -116,9 +116,10 @@ def parse() -> argparse.Namespace:
     p.add_argument(
         "--workload",
         default="c4",
-        choices=["c4", "copy", "c1", "c2", "c3", "c5"],
+        choices=["c4", "copy", "c1", "c2", "c3", "c5", "sizes"],
         help="c4: the headline attention step; copy: a plain 256 MiB device copy kernel, the "
-        "known-size reference that scales rocprofv3's FETCH_SIZE/WRITE_SIZE counters",
+        "known-size reference that scales rocprofv3's FETCH_SIZE/WRITE_SIZE counters; sizes: two "
+        "emitted kernels of the GPT step's kinds timed at launch sizes from 8 to 512 MiB",
     )
     return p.parse_args()
 
@@ -234,6 +235,39 @@ def copy_probe(steps: int) -> int:
     ms = ev.ms(0, 1) / steps
     print(json.dumps({"probe": "copy", "bytes_read": nbytes, "bytes_written": nbytes, "ms": round(ms, 4),
                       "GB_s": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+    return 0
+
+
+def size_probe(steps: int) -> int:
+    """The rate of two emitted kernels of the GPT step's kinds against their launch size: an
+    elementwise nest (x * 2 over bf16 rows of 512) and a LayerNorm row program (float32
+    statistics, bf16 in and out, width 512), each at 4096 to 262144 rows (8 to 512 MiB moved).
+    Each is timed with events only at its ends, clock settled first. Prints a JSON line per
+    kernel and size (not bench lines)."""
+    from limn_amd.hip.device import HipDevice
+    from limn_amd.seam import device as limn_device
+    from limn_amd.seam import Tensor, bfloat16, float32, nn
+
+    dev = HipDevice()
+    limn_device.active_device = dev
+    rng = np.random.default_rng(3)
+    ln = nn.LayerNorm(512)
+    for rows in (4096, 8192, 16384, 32768, 65536, 131072, 262144):
+        x = Tensor(rng.standard_normal((rows, 512)).astype(np.float32), dtype=bfloat16)
+        for name, node in (("elementwise", (x * 2.0).node), ("layernorm_rows", ln(x.cast(float32)).cast(bfloat16).node)):
+            plan, sources = record_plan(dev, [node])
+            settle(dev, lambda: timed_calls(dev, plan, sources, NoEvents(), 0))
+            ev = Events(dev.api, 2 * steps)
+            for s_ in range(steps):
+                ev.record(2 * s_)
+                timed_calls(dev, plan, sources, NoEvents(), 0)
+                ev.record(2 * s_ + 1)
+            dev.finish()
+            ms = float(np.median([ev.ms(2 * s_, 2 * s_ + 1) for s_ in range(steps)]))
+            moved = 2 * rows * 512 * 2  # bf16 in and out
+            launched = sum(1 for call in plan.calls if not getattr(call.fn, "launches_nothing", False))
+            print(json.dumps({"probe": "sizes", "kernel": name, "rows": rows, "launches": launched, "bytes": moved,
+                              "us": round(ms * 1e3, 2), "TB_s": round(moved / (ms * 1e-3) / 1e12, 2)}), flush=True)
     return 0
 
 
@@ -798,6 +832,8 @@ def main() -> int:
         return summarize(args.summarize)
     if args.workload == "copy":
         return copy_probe(args.steps)
+    if args.workload == "sizes":
+        return size_probe(args.steps)
     if args.workload == "c1":
         from limn_amd.hip.device import HipDevice
 
