@@ -150,6 +150,11 @@ def test_rows_family_key_mask(hipdev, shapes, causal, live):
 # MFMA family: bf16/f16 at D = 64 and 128
 MFMA_CASES = {
     "d64_ragged": ((2, 2, 200, 64), (2, 2, 200, 64), (2, 2, 200, 64)),
+    # causal D = 64 workgroups take a 128-row block and its mirror: three blocks leave the middle
+    # one paired with itself, four are the GPT step's heads (512 rows), five end ragged
+    "d64_three_blocks": ((1, 2, 384, 64), (1, 2, 384, 64), (1, 2, 384, 64)),
+    "d64_four_blocks": ((2, 1, 512, 64), (2, 1, 512, 64), (2, 1, 512, 64)),
+    "d64_five_ragged": ((1, 1, 600, 64), (1, 1, 600, 64), (1, 1, 600, 64)),
     "d128_two_blocks": ((1, 2, 256, 128), (1, 2, 256, 128), (1, 2, 256, 128)),
     "d128_ragged": ((2, 1, 333, 128), (2, 1, 333, 128), (2, 1, 333, 128)),
     # long heads: 10 and 13 query tiles per key block, tile loops unrolled by two with an odd
